@@ -1,0 +1,131 @@
+// Device helpers shared by every gfx950 kernel of the skinny BF16 projection path.
+//
+// BF16 travels as raw 16-bit patterns (uint16_t); arithmetic is FP32. The
+// rounding rule is round-to-nearest-even with every NaN mapped to 0x7FC0, the
+// rule torch and the reference's Triton casts use (engine/kernels/linear.py:1-6).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ftk {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Low / high BF16 of a packed pair, widened exactly to FP32.
+__device__ __forceinline__ float lo_f32(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t pair) { return __uint_as_float(pair & 0xFFFF0000u); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// FP32 -> nearest BF16 value, kept in FP32 (one rounding).
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
+
+// acc + sum over 8 BF16 products. The products are exact in FP32; v_dot2 adds
+// them with FP32 accumulation, so this is an FP32-accumulated dot in some order.
+// (Elements are copied to scalars first: bit-casting a vector element
+// expression directly made this clang read element 0 for every element.)
+__device__ __forceinline__ float dot8(u32x4_t w, u32x4_t x, float acc) {
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+  const uint32_t x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w0), as_bf16x2(x0), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w1), as_bf16x2(x1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w2), as_bf16x2(x2), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w3), as_bf16x2(x3), acc, false);
+  return acc;
+}
+
+// Streaming 16-byte load: weights are read exactly once per call.
+__device__ __forceinline__ u32x4_t load_stream16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+
+__device__ __forceinline__ u32x4_t load16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+// DPP lane exchange: lanes whose row is masked off read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; the total lands in lane 63.
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+  v += dpp<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp<0x140, 0xF>(v);  // row_mirror
+  v += dpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Wave total, made uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = wave_sum_to_last(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Greedy-argmax key: larger key = larger BF16 value, then lower index.
+// NaN counts as the maximum (torch.argmax), and -0 equals +0.
+__device__ __forceinline__ uint32_t orderable(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) u = 0x7FC00000u;
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float from_orderable(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float value, uint32_t index) {
+  return (static_cast<unsigned long long>(orderable(value)) << 32) | (0xFFFFFFFFu - index);
+}
+
+__device__ __forceinline__ uint32_t key_index(unsigned long long key) {
+  return 0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull);
+}
+
+__device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ float silu_f32(float g) {
+  return g / (1.0f + expf(-g));
+}
+
+// SwiGLU on FP32 sums: gate and up are rounded to BF16 first, SiLU's output is
+// rounded to BF16, and the product is rounded once more (engine/kernels/swiglu.py:20-24).
+__device__ __forceinline__ uint32_t swiglu_bf16(float gate_sum, float up_sum) {
+  const float g = round_bf16(gate_sum);
+  const float u = round_bf16(up_sum);
+  const float a = round_bf16(silu_f32(g));
+  return f32_to_bf16(a * u);
+}
+
+}  // namespace ftk

@@ -1,0 +1,322 @@
+// M = 1..4 skinny BF16 projection as an HBM-streaming GEMV for gfx950.
+//
+// Computes the sums of engine/kernels/linear.py:27-47 (_gemv): y[m, n] =
+// bf16(sum_k f32(x[m, k]) * f32(W[n, k])), FP32 accumulation, one rounding,
+// with three fused extras the reference runs as separate launches:
+//   * RMSNorm prologue (engine/kernels/rmsnorm.py:21-46 cast order),
+//   * SwiGLU epilogue over cat(W_gate, W_up) (engine/kernels/swiglu.py:13-24),
+//   * greedy-argmax epilogue (engine/kernels/argmax.py:19-48, :73-106).
+//
+// Layout and schedule:
+//   * A workgroup is 4 waves. It stages x (normalised when the prologue is on)
+//     in LDS once, then walks row tiles grid-stride.
+//   * A wave owns RPW whole weight rows per tile. Lane l reads 16-byte chunks
+//     l, l+64, l+128, ... of each row, so every wave-wide load is 1 KiB of
+//     contiguous HBM; loads are non-temporal (weights are read exactly once).
+//   * Products use v_dot2_f32_bf16 (two exact BF16 products + FP32 add per
+//     instruction, no unpacking), accumulating per lane in FP32.
+//   * Each row's 64 lane partials are summed with a DPP tree; the result is
+//     rounded to BF16 once.
+//   * Argmax: per-row keys (orderable BF16 value, inverted index) reduced by
+//     max within the wave, the workgroup, then one 64-bit atomicMax per
+//     workgroup and input row; the last workgroup (ticket counter) writes the
+//     ids and clears the workspace. max is order-independent, so the result
+//     is deterministic and equals torch.argmax's lowest-index rule.
+#include "ftk_device.h"
+#include "ftk_internal.h"
+
+namespace ftk {
+
+template <int MR, int RPW, int U, bool PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
+  extern __shared__ u32x4_t xs[];  // x as [MR][K/8] chunks of 8 BF16
+  __shared__ float red[kWaves][MR];
+  __shared__ unsigned long long best_lds[kWaves][MR];
+  __shared__ int is_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int K = a.K;
+  const int KC = K >> 3;           // 16-byte chunks per row
+
+  // ---- stage x into LDS (and the RMSNorm prologue) ----------------------
+  float ss[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    ss[m] = 0.f;
+    for (int c = tid; c < KC; c += kThreads) {
+      const u32x4_t v = load16(a.x + (size_t)m * K + (size_t)c * 8);
+      xs[m * KC + c] = v;
+      if constexpr (PRO) {
+        const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
+          ss[m] += lo * lo;
+          ss[m] += hi * hi;
+        }
+      }
+    }
+  }
+  if constexpr (PRO) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float s = wave_sum(ss[m]);
+      if (lane == 0) red[wave][m] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      // Same fixed order in every workgroup: every workgroup normalises identically.
+      const float total = ((red[0][m] + red[1][m]) + red[2][m]) + red[3][m];
+      const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
+      for (int c = tid; c < KC; c += kThreads) {
+        const u32x4_t v = xs[m * KC + c];
+        const u32x4_t g = load16(a.gamma + (size_t)c * 8);
+        const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t ge[4] = {g.x, g.y, g.z, g.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // bf16(x * rsqrt) first, then the gamma multiply, rounded again.
+          const float nlo = round_bf16(lo_f32(e[i]) * scale);
+          const float nhi = round_bf16(hi_f32(e[i]) * scale);
+          o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
+        }
+        xs[m * KC + c] = u32x4_t{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- stream the weight rows ----------------------------------------------
+  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per wave per tile
+  const int outputs = gemv_outputs(EPI, a.N);
+  unsigned long long best[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) best[m] = 0ull;
+
+  // This lane's first chunk of every weight row the wave reads for ``tile``.
+  auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int col = gemv_output(tile, wave, p, PW);
+      const int c = col < outputs ? col : outputs - 1;  // clamp: loads stay in bounds
+      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + lane * 8;
+      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + lane * 8;
+    }
+  };
+
+  // Reduce the lane partials of ``tile``, run the epilogue, clear the accumulators.
+  auto finish = [&](int tile, float (&acc)[RPW][MR]) {
+    float tot[RPW][MR];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        tot[r][m] = wave_sum(acc[r][m]);
+        acc[r][m] = 0.f;
+      }
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int col = gemv_output(tile, wave, p, PW);
+      if (col >= outputs) continue;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if constexpr (EPI == EPI_STORE) {
+          if (lane == 0) a.y[(size_t)m * a.N + col] = (uint16_t)f32_to_bf16(tot[p][m]);
+        } else if constexpr (EPI == EPI_SWIGLU) {
+          if (lane == 0) a.y[(size_t)m * (a.N / 2) + col] = (uint16_t)swiglu_bf16(tot[p][m], tot[PW + p][m]);
+        } else {
+          const uint32_t bits = f32_to_bf16(tot[p][m]);
+          if (a.y != nullptr && lane == 0) a.y[(size_t)m * a.N + col] = (uint16_t)bits;
+          best[m] = key_max(best[m], argmax_key(bf16_to_f32(bits), (uint32_t)col));
+        }
+      }
+    }
+  };
+
+  float acc[RPW][MR];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+
+  const uint16_t* wr[RPW];
+  if (KC % (64 * U) == 0) {
+    // Every lane's chunks are in range: batches of U x RPW 16-byte loads, all
+    // issued before the first is consumed. Memory parallelism comes from the
+    // batch size and from the other waves resident on the SIMD.
+    const int NB = KC / (64 * U);
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+      row_ptrs(tile, wr);
+      for (int b = 0; b < NB; ++b) {
+        u32x4_t wv[U][RPW];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream16(wr[r] + (size_t)(b * U + u) * 512);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = (b * U + u) * 64 + lane;
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            const u32x4_t xv = xs[m * KC + c];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) acc[r][m] = dot8(wv[u][r], xv, acc[r][m]);
+          }
+        }
+      }
+      finish(tile, acc);
+    }
+  } else {
+    // Ragged chunk count: per-lane bounds checks.
+    const int C = (KC + 63) >> 6;
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+      row_ptrs(tile, wr);
+      for (int j = 0; j < C; ++j) {
+        const int c = j * 64 + lane;
+        if (c < KC) {
+          u32x4_t wv[RPW];
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) wv[r] = load_stream16(wr[r] + (size_t)j * 512);
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            const u32x4_t xv = xs[m * KC + c];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) acc[r][m] = dot8(wv[r], xv, acc[r][m]);
+          }
+        }
+      }
+      finish(tile, acc);
+    }
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m) best_lds[wave][m] = best[m];
+    }
+    __syncthreads();
+    if (tid < MR) {
+      unsigned long long k = best_lds[0][tid];
+      for (int w = 1; w < kWaves; ++w) k = key_max(k, best_lds[w][tid]);
+      atomicMax(a.keys + tid, k);
+      __threadfence();
+    }
+    __syncthreads();
+    if (tid == 0) is_last = (atomicAdd(a.ticket, 1u) == gridDim.x - 1);
+    __syncthreads();
+    if (is_last) {
+      __threadfence();
+      if (tid < MR) {
+        const unsigned long long k = atomicMax(a.keys + tid, 0ull);
+        const uint32_t idx = key_index(k);
+        if (a.ids_bytes == 8)
+          reinterpret_cast<int64_t*>(a.ids)[tid] = (int64_t)idx;
+        else
+          reinterpret_cast<int32_t*>(a.ids)[tid] = (int32_t)idx;
+        if (a.top != nullptr) a.top[tid] = from_orderable((uint32_t)(k >> 32));
+        atomicExch(a.keys + tid, 0ull);
+      }
+      if (tid == 0) atomicExch(a.ticket, 0u);
+    }
+  }
+}
+
+// ---- ragged / unaligned fallback: one wave per weight row, scalar loads --------
+template <int MAXM>
+__global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ w,
+                                                                uint16_t* __restrict__ y, int M, int N, int K) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= N) return;  // whole wave leaves together; no barrier below
+  float acc[MAXM];
+#pragma unroll
+  for (int m = 0; m < MAXM; ++m) acc[m] = 0.f;
+  const uint16_t* wr = w + (size_t)row * K;
+  for (int k = lane; k < K; k += 64) {
+    const float wk = bf16_to_f32(wr[k]);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+      if (m < M) acc[m] += bf16_to_f32(x[(size_t)m * K + k]) * wk;
+  }
+#pragma unroll
+  for (int m = 0; m < MAXM; ++m) {
+    if (m < M) {
+      const float s = wave_sum(acc[m]);
+      if (lane == 0) y[(size_t)m * N + row] = (uint16_t)f32_to_bf16(s);
+    }
+  }
+}
+
+// ---- dispatch -------------------------------------------------------------------
+
+typedef void (*GemvKernel)(ProjArgs, int);
+
+#define FTK_GEMV_RU(MR, PRO, EPI)                                                             \
+  if (rpw == 2 && unroll == 4) return gemv_kernel<MR, 2, 4, PRO, EPI>;                        \
+  if (rpw == 4 && unroll == 2) return gemv_kernel<MR, 4, 2, PRO, EPI>;                        \
+  if (rpw == 4 && unroll == 4) return gemv_kernel<MR, 4, 4, PRO, EPI>;                        \
+  if (rpw == 8 && unroll == 1) return gemv_kernel<MR, 8, 1, PRO, EPI>;                        \
+  if (rpw == 8 && unroll == 2) return gemv_kernel<MR, 8, 2, PRO, EPI>;                        \
+  return nullptr;
+
+#define FTK_GEMV_EPI(MR, PRO)                         \
+  switch (epi) {                                      \
+    case EPI_STORE: { FTK_GEMV_RU(MR, PRO, EPI_STORE) } \
+    case EPI_SWIGLU: { FTK_GEMV_RU(MR, PRO, EPI_SWIGLU) } \
+    case EPI_ARGMAX: { FTK_GEMV_RU(MR, PRO, EPI_ARGMAX) } \
+  }                                                   \
+  return nullptr;
+
+template <int MR>
+static GemvKernel pick_mr(int rpw, int unroll, bool pro, int epi) {
+  if (pro) {
+    FTK_GEMV_EPI(MR, true)
+  } else {
+    FTK_GEMV_EPI(MR, false)
+  }
+}
+
+static GemvKernel pick_gemv(int M, int rpw, int unroll, bool pro, int epi) {
+  switch (M) {
+    case 1: return pick_mr<1>(rpw, unroll, pro, epi);
+    case 2: return pick_mr<2>(rpw, unroll, pro, epi);
+    case 3: return pick_mr<3>(rpw, unroll, pro, epi);
+    case 4: return pick_mr<4>(rpw, unroll, pro, epi);
+  }
+  return nullptr;
+}
+
+bool gemv_supported(int M, int rpw, int unroll, int epi) {
+  return pick_gemv(M, rpw, unroll, false, epi) != nullptr;
+}
+
+hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& s, hipStream_t stream) {
+  GemvKernel k = pick_gemv(a.M, s.rpw, s.unroll, a.gamma != nullptr, epi);
+  if (k == nullptr) return hipErrorInvalidValue;
+  if (s.lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s.lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k, dim3(s.grid), dim3(kThreads), s.lds, stream, a, s.tiles);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
+                               hipStream_t stream) {
+  const int grid = (N + kWaves - 1) / kWaves;
+  if (M <= 4)
+    hipLaunchKernelGGL(gemm_generic_kernel<4>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+  else if (M <= 16)
+    hipLaunchKernelGGL(gemm_generic_kernel<16>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+  else
+    hipLaunchKernelGGL(gemm_generic_kernel<32>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+  return hipGetLastError();
+}
+
+}  // namespace ftk

@@ -1,0 +1,178 @@
+// Standalone operators of the path, for callers that keep them separate:
+//   rms_norm       engine/kernels/rmsnorm.py:21-72
+//   add_rms_norm   engine/kernels/rmsnorm.py:75-125 (BF16 input or FP32 split partials)
+//   swiglu         engine/kernels/swiglu.py:13-40   (BF16 input or FP32 split partials)
+//   argmax         engine/kernels/argmax.py:19-70   (lowest index on ties)
+//   merge_splits   engine/kernels/linear.py:81-93, engine/kernels/merged.py:37-45
+// These are small, launch-bound kernels; the projections fold the norm, SwiGLU
+// and argmax into themselves and do not need them.
+#include "ftk_device.h"
+#include "ftk_internal.h"
+
+namespace ftk {
+
+// Sum over the workgroup in a fixed order (wave DPP tree, then waves 0..3).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float total = ((red[0] + red[1]) + red[2]) + red[3];
+  __syncthreads();
+  return total;
+}
+
+// Value of element ``off`` of a BF16 tensor, or bf16(sum of FP32 partials in split order).
+__device__ __forceinline__ float merged_value(const void* src, int splits, int64_t stride, int64_t off) {
+  if (splits == 0) return bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[off]);
+  const float* p = reinterpret_cast<const float*>(src);
+  float total = p[off];
+  for (int s = 1; s < splits; ++s) total += p[(int64_t)s * stride + off];
+  return round_bf16(total);
+}
+
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __restrict__ x, int64_t row_stride,
+                                                            const uint16_t* __restrict__ gamma,
+                                                            uint16_t* __restrict__ y, int cols, float eps) {
+  __shared__ float red[kWaves];
+  const uint16_t* xr = x + (int64_t)blockIdx.x * row_stride;
+  uint16_t* yr = y + (int64_t)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float v = bf16_to_f32(xr[c]);
+    ss += v * v;
+  }
+  const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float n = round_bf16(bf16_to_f32(xr[c]) * scale);
+    yr[c] = (uint16_t)f32_to_bf16(n * bf16_to_f32(gamma[c]));
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(const void* __restrict__ x, int splits,
+                                                                int64_t split_stride,
+                                                                const uint16_t* __restrict__ residual,
+                                                                const uint16_t* __restrict__ gamma,
+                                                                uint16_t* __restrict__ y, uint16_t* __restrict__ sum,
+                                                                int cols, float eps) {
+  __shared__ float red[kWaves];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    // The residual addition is a BF16 tensor operation: round the sum first.
+    const float s = round_bf16(merged_value(x, splits, split_stride, base + c) + bf16_to_f32(residual[base + c]));
+    sum[base + c] = (uint16_t)f32_to_bf16(s);
+    ss += s * s;
+  }
+  const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float s = round_bf16(merged_value(x, splits, split_stride, base + c) + bf16_to_f32(residual[base + c]));
+    const float n = round_bf16(s * scale);
+    y[base + c] = (uint16_t)f32_to_bf16(n * bf16_to_f32(gamma[c]));
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(const void* __restrict__ packed, int splits,
+                                                          int64_t split_stride, uint16_t* __restrict__ out,
+                                                          int width, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int64_t row = i / width, j = i - row * width;
+  const int64_t g_off = row * 2 * width + j;
+  const float g = merged_value(packed, splits, split_stride, g_off);
+  const float u = merged_value(packed, splits, split_stride, g_off + width);
+  out[i] = (uint16_t)swiglu_bf16(g, u);
+}
+
+// One workgroup per (row, column block of 8192): block key max, one atomicMax
+// per workgroup and row, the last workgroup writes ids and clears the workspace.
+constexpr int kArgmaxBlock = 8192;
+
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int vocab, void* ids,
+                                                          int ids_bytes, float* top, unsigned long long* keys,
+                                                          unsigned int* ticket, int rows) {
+  __shared__ unsigned long long red[kThreads];
+  __shared__ int is_last;
+  const int row = blockIdx.y;
+  const int begin = blockIdx.x * kArgmaxBlock;
+  const int end = min(begin + kArgmaxBlock, vocab);
+  const uint16_t* lr = logits + (int64_t)row * vocab;
+  unsigned long long best = 0ull;
+  for (int c = begin + threadIdx.x; c < end; c += kThreads)
+    best = key_max(best, argmax_key(bf16_to_f32(lr[c]), (uint32_t)c));
+  red[threadIdx.x] = best;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = key_max(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    atomicMax(keys + row, red[0]);
+    __threadfence();
+    is_last = (atomicAdd(ticket, 1u) == gridDim.x * gridDim.y - 1);
+  }
+  __syncthreads();
+  if (is_last) {
+    __threadfence();
+    for (int r = threadIdx.x; r < rows; r += kThreads) {
+      const unsigned long long k = atomicMax(keys + r, 0ull);
+      const uint32_t idx = key_index(k);
+      if (ids_bytes == 8)
+        reinterpret_cast<int64_t*>(ids)[r] = (int64_t)idx;
+      else
+        reinterpret_cast<int32_t*>(ids)[r] = (int32_t)idx;
+      if (top != nullptr) top[r] = from_orderable((uint32_t)(k >> 32));
+      atomicExch(keys + r, 0ull);
+    }
+    if (threadIdx.x == 0) atomicExch(ticket, 0u);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void merge_splits_kernel(const float* __restrict__ partial, int splits,
+                                                                int64_t count, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= count) return;
+  float total = partial[i];
+  for (int s = 1; s < splits; ++s) total += partial[(int64_t)s * count + i];
+  out[i] = (uint16_t)f32_to_bf16(total);
+}
+
+hipError_t launch_rms_norm(const uint16_t* x, int64_t row_stride, const uint16_t* gamma, uint16_t* y, int rows,
+                           int cols, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, row_stride, gamma, y, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rms_norm(const void* x, int splits, int64_t split_stride, const uint16_t* residual,
+                               const uint16_t* gamma, uint16_t* y, uint16_t* sum, int rows, int cols, float eps,
+                               hipStream_t stream) {
+  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, splits, split_stride, residual,
+                     gamma, y, sum, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const void* packed, int splits, int64_t split_stride, uint16_t* out, int rows, int width,
+                         hipStream_t stream) {
+  const int64_t total = (int64_t)rows * width;
+  const int64_t grid = (total + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, packed, splits, split_stride,
+                     out, width, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids, int ids_bytes, float* top,
+                         unsigned long long* keys, unsigned int* ticket, hipStream_t stream) {
+  const int blocks = (vocab + kArgmaxBlock - 1) / kArgmaxBlock;
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, ids, ids_bytes,
+                     top, keys, ticket, rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge_splits(const float* partial, int splits, int64_t count, uint16_t* out, hipStream_t stream) {
+  const int64_t grid = (count + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(merge_splits_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, partial, splits, count,
+                     out);
+  return hipGetLastError();
+}
+
+}  // namespace ftk

@@ -1,0 +1,75 @@
+// Tiling arithmetic shared by the kernels (device) and the launch planner (host).
+//
+// The kernels and the exported plan/coverage functions call the same inline
+// functions, so a CPU test of the coverage function checks the mapping the GPU
+// actually runs: every output written by exactly one (workgroup, tile, wave,
+// slot), every weight row and K chunk in bounds.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define FTK_HD __host__ __device__ __forceinline__
+#else
+#define FTK_HD inline
+#endif
+
+namespace ftk {
+
+constexpr int kWaves = 4;           // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+
+enum Epilogue : int {
+  EPI_STORE = 0,   // y[m, n] = bf16(sum)
+  EPI_SWIGLU = 1,  // y[m, j] = swiglu(sum(gate row j), sum(up row I + j))
+  EPI_ARGMAX = 2,  // logits (optional) + greedy id per input row
+};
+
+// ---- M <= 4: HBM-streaming GEMV (one wave owns whole weight rows) --------
+
+// Outputs one wave produces per tile: RPW rows, or RPW/2 gate/up pairs.
+FTK_HD int gemv_per_wave(int epi, int rpw) { return epi == EPI_SWIGLU ? rpw / 2 : rpw; }
+
+// Output columns: N (store / argmax) or I = N / 2 (SwiGLU pairs).
+FTK_HD int gemv_outputs(int epi, int n_rows) { return epi == EPI_SWIGLU ? n_rows / 2 : n_rows; }
+
+FTK_HD int gemv_tiles(int epi, int n_rows, int rpw) {
+  const int per_tile = kWaves * gemv_per_wave(epi, rpw);
+  return (gemv_outputs(epi, n_rows) + per_tile - 1) / per_tile;
+}
+
+// Output column of (tile, wave, slot).
+FTK_HD int gemv_output(int tile, int wave, int slot, int per_wave) {
+  return (tile * kWaves + wave) * per_wave + slot;
+}
+
+// Weight row feeding output ``col``: the row itself, or for SwiGLU the gate row
+// (half 0) or the up row I + col (half 1) of cat(W_gate, W_up) (engine/layers.py:92-95).
+FTK_HD int gemv_weight_row(int epi, int col, int half, int n_rows) {
+  return epi == EPI_SWIGLU ? col + half * (n_rows / 2) : col;
+}
+
+// ---- M >= 4: BF16 MFMA skinny GEMM (16 weight rows per wave subtile) ------
+
+constexpr int kMfmaRows = 16;       // weight rows per MFMA subtile (v_mfma_f32_16x16x32_bf16)
+constexpr int kMfmaK = 32;          // K per MFMA step
+
+// Persistent launch: the fewest programs that keep the deepest walk at
+// ceil(tiles / units) (the rule of engine/kernels/gemm.py:330-338).
+FTK_HD int persistent_programs(int tiles, int units) {
+  if (tiles <= 0 || units <= 0) return 0;
+  const int depth = (tiles + units - 1) / units;
+  return (tiles + depth - 1) / depth;
+}
+
+// Largest split count <= wanted whose chunks tile K with whole block_k blocks
+// (engine/kernels/gemm.py:428-433).
+FTK_HD int exact_splits(int k, int block_k, int wanted) {
+  if (k % block_k) return wanted;
+  const int blocks = k / block_k;
+  for (int s = wanted; s > 1; --s)
+    if (blocks % s == 0) return s;
+  return 1;
+}
+
+}  // namespace ftk

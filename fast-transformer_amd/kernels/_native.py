@@ -1,0 +1,142 @@
+"""ctypes binding of libftk.so, the gfx950 HIP library behind every kernel in this package.
+
+The library's C ABI is declared in include/ftk.h. Tensors cross it as raw
+device pointers, streams as hipStream_t handles taken from torch's current
+stream. There is no fallback: if the library is missing or fails to load,
+every call raises.
+"""
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).with_name("libftk.so")
+
+FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = range(5)
+EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
+KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC = range(4)
+MAX_ROWS = 32
+
+_c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+
+class Config(ctypes.Structure):
+    """ftk_config: a launch choice (kind, rows_per_wave, unroll, groups_per_cu); zeros = planner default."""
+
+    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("groups_per_cu", _int)]
+
+    def key(self):
+        return (self.kind, self.rows_per_wave, self.unroll, self.groups_per_cu)
+
+    def __repr__(self):
+        return f"Config{self.key()}"
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("grid", _int), ("tiles", _int),
+                ("threads", _int), ("lds_bytes", _i64)]
+
+
+# name -> (restype, argtypes), exactly the declarations of include/ftk.h
+SIGNATURES = {
+    "ftk_version": (ctypes.c_char_p, []),
+    "ftk_status_string": (ctypes.c_char_p, [_int]),
+    "ftk_last_hip_error": (_int, []),
+    "ftk_device_compute_units": (_int, []),
+    "ftk_linear_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
+    "ftk_rms_norm_linear_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                        _c_void_p]),
+    "ftk_gate_up_swiglu_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                       _c_void_p]),
+    "ftk_lm_head_argmax_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _c_void_p, _int,
+                                       _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
+    "ftk_project_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64, _int,
+                                _c_void_p, _int, _c_void_p, _c_void_p, _i64, ctypes.POINTER(Config), _c_void_p]),
+    "ftk_rms_norm_bf16": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _float, _c_void_p]),
+    "ftk_add_rms_norm_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                     _i64, _float, _c_void_p]),
+    "ftk_swiglu_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _i64, _i64, _c_void_p]),
+    "ftk_argmax_bf16": (_int, [_c_void_p, _i64, _i64, _c_void_p, _int, _c_void_p, _c_void_p, _i64, _c_void_p]),
+    "ftk_merge_splits_bf16": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "ftk_argmax_workspace_bytes": (_i64, [_i64]),
+    "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
+    "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
+                                 ctypes.POINTER(_i64)]),
+}
+
+_LIB = None
+_LOCK = threading.Lock()
+
+
+class FtkError(RuntimeError):
+    def __init__(self, name, status, hip_error=0):
+        self.status, self.hip_error = status, hip_error
+        text = lib().ftk_status_string(status).decode()
+        extra = f" (hipError {hip_error})" if status == FTK_ERR_HIP else ""
+        super().__init__(f"{name}: {text}{extra}")
+
+
+def lib():
+    """The loaded library (loaded once). Raises if libftk.so is missing: there is no fallback."""
+    global _LIB
+    if _LIB is None:
+        with _LOCK:
+            if _LIB is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build it with `python fast-transformer_amd/build.py` "
+                        "(or __graft_entry__.build()); these kernels have no fallback")
+                # torch first: the library must bind to the HIP runtime torch already loaded.
+                handle = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+                for name, (restype, argtypes) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype, fn.argtypes = restype, argtypes
+                _LIB = handle
+    return _LIB
+
+
+def call(name, *args):
+    """Call an ftk entry point; raise FtkError on any status but FTK_OK."""
+    status = getattr(lib(), name)(*args)
+    if status != FTK_OK:
+        raise FtkError(name, status, lib().ftk_last_hip_error() if status == FTK_ERR_HIP else 0)
+
+
+def try_call(name, *args):
+    """Call an ftk entry point; return its status, raising only on launch failure."""
+    status = getattr(lib(), name)(*args)
+    if status == FTK_ERR_HIP:
+        raise FtkError(name, status, lib().ftk_last_hip_error())
+    return status
+
+
+def stream_of(tensor):
+    """hipStream_t of torch's current stream on the tensor's device."""
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def ptr(tensor):
+    return ctypes.c_void_p(tensor.data_ptr()) if tensor is not None else None
+
+
+def require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("these kernels run on the GPU: got a tensor on " + str(t.device))
+
+
+_WORKSPACES = {}
+
+
+def argmax_workspace(device, rows):
+    """Per-device zeroed argmax workspace (the kernels leave it zeroed after each call)."""
+    need = int(lib().ftk_argmax_workspace_bytes(rows))
+    ws = _WORKSPACES.get(device)
+    if ws is None or ws.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("argmax workspace must be allocated during eager warmup, before graph capture")
+        ws = torch.zeros(max(need, 4096), dtype=torch.uint8, device=device)
+        _WORKSPACES[device] = ws
+    return ws

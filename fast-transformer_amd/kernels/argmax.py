@@ -1,0 +1,99 @@
+"""Greedy token ids from BF16 logits, lowest index on ties (engine/kernels/argmax.py:1-167).
+
+``argmax(logits, block=8192, top=None)``, ``fused_argmax(x, weight, ...)`` and
+``greedy_tokens(x, weight, linear, top=None)`` keep the reference's
+signatures and int64 results. Ties resolve to the lowest index and NaN counts
+as the maximum, torch.argmax's rule; BF16 -> FP32 is exact, so the answer is
+identical to torch.argmax of the BF16 logits.
+
+Device scheme: each workgroup reduces its logits to a 64-bit key (orderable
+BF16 value << 32 | ~index) and folds it into a per-row slot with one atomicMax;
+the last workgroup to finish (ticket counter) writes the ids and clears the
+workspace. max is order-independent, so results are deterministic.
+
+``lm_head_argmax`` is the fused final-norm + lm_head + argmax kernel: the
+vocabulary GEMV rounds each logit to BF16 and reduces it in its epilogue,
+optionally writing the logits and the winning FP32 logit (``top``).
+"""
+
+import torch
+
+from kernels import _native
+
+
+def argmax(logits, block=8192, top=None):
+    """int64 argmax over the last dimension of BF16 logits [..., V]; with ``top`` also the winning logit (FP32)."""
+    if logits.dtype != torch.bfloat16:
+        return logits.argmax(dim=-1)
+    _native.require_gpu(logits, top)
+    logits = logits.contiguous()
+    vocab = logits.shape[-1]
+    rows = logits.numel() // vocab
+    out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=logits.device)
+    ws = _native.argmax_workspace(logits.device, rows)
+    if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < rows):
+        raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
+    _native.call("ftk_argmax_bf16", _native.ptr(logits), rows, vocab, _native.ptr(out), 8, _native.ptr(top),
+                 _native.ptr(ws), ws.numel(), _native.stream_of(logits))
+    return out
+
+
+def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None, ids_dtype=torch.int64,
+                   config=None):
+    """(ids, logits or None): greedy ids of rms_norm?(x) @ weight.T in one projection kernel.
+
+    Ties go to the lowest index of the BF16-rounded logits. Returns None for
+    shapes the fused kernel does not take (the caller then projects and calls ``argmax``).
+    """
+    _native.require_gpu(x, weight, norm_weight, top)
+    shape = x.shape
+    flat = x.reshape(-1, shape[-1]).contiguous()
+    m, k = flat.shape
+    v = weight.shape[0]
+    ids = torch.empty(shape[:-1], dtype=ids_dtype, device=x.device)
+    out = torch.empty((*shape[:-1], v), dtype=torch.bfloat16, device=x.device) if logits else None
+    ws = _native.argmax_workspace(x.device, m)
+    ids_bytes = {torch.int64: 8, torch.int32: 4}[ids_dtype]
+    status = _native.try_call(
+        "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
+        _native.ptr(out), m, v, k, _native.EPI_ARGMAX, _native.ptr(ids), ids_bytes, _native.ptr(top),
+        _native.ptr(ws), ws.numel(), config, _native.stream_of(flat))
+    if status == _native.FTK_ERR_UNSUPPORTED:
+        return None
+    if status != _native.FTK_OK:
+        raise _native.FtkError("ftk_project_bf16", status)
+    return ids, out
+
+
+def fused_argmax(x, weight, block_n=64, block_k=128):
+    """argmax(x @ weight.T) for <= 32 BF16 rows without materializing the logits; None if not applicable.
+
+    (argmax.py:112-129.) ``block_n``/``block_k`` are accepted for signature parity;
+    the HIP kernel needs neither N nor K to be a multiple of anything but K % 8.
+    """
+    rows = x.numel() // x.shape[-1]
+    if rows > _native.MAX_ROWS or x.dtype != torch.bfloat16 or not weight.is_contiguous():
+        return None
+    result = lm_head_argmax(x, weight, logits=False)
+    return None if result is None else result[0]
+
+
+def greedy_tokens(x, weight, linear, top=None):
+    """Greedy token per row of x @ weight.T (argmax.py:132-167).
+
+    With ``top`` the caller also wants the logits and the winning logit:
+    returns (ids, logits). When ``linear`` is this package's projection, the
+    fused lm_head kernel does both in one launch; any other ``linear`` is
+    honoured by projecting with it and calling ``argmax``.
+    """
+    from kernels import linear as _linear_module
+
+    if linear is _linear_module.linear:
+        result = lm_head_argmax(x, weight, logits=top is not None, top=top)
+        if result is not None:
+            ids, logits = result
+            return (ids, logits) if top is not None else ids
+    logits = linear(x, weight)
+    if top is not None:
+        return argmax(logits, top=top), logits
+    return argmax(logits)

@@ -1,0 +1,179 @@
+"""BF16 skinny projections y = x @ W.T for M <= 32 rows, on gfx950 HIP kernels.
+
+Drop-in for engine/kernels/linear.py: ``linear(x, weight, split_ok=False)``,
+``keep_native(rows, weight)`` and ``MAX_ROWS`` keep the reference's names,
+argument meaning and fallback rule (linear.py:484-523). FP32 accumulation and
+one rounding to BF16 (linear.py:1-6). Under them:
+
+  * M <= 4: an HBM-streaming GEMV (x resident in LDS, 16-byte non-temporal
+    weight loads, v_dot2_f32_bf16, DPP reductions);
+  * any other shape: the kind the C library's planner picks (ragged K or an
+    unaligned pointer takes a generic kernel with scalar loads).
+
+``split_ok`` is accepted for signature compatibility. The result is always a
+contiguous BF16 tensor, which the reference allows ("may be" a Split,
+linear.py:490): split-K is finished inside the kernel.
+
+Beyond the reference's surface, the fused forms of the path live here too:
+``rms_norm_linear`` (RMSNorm prologue + projection), and in swiglu.py /
+argmax.py the SwiGLU and greedy-argmax epilogues.
+"""
+
+import os
+import statistics
+
+import torch
+from torch.nn import functional as F
+
+from kernels import _native
+from kernels.tune import register
+
+#: Verify blocks of up to 32 rows still read each weight once per step (linear.py:340-343).
+MAX_ROWS = _native.MAX_ROWS
+
+#: (device, rows, N, K) -> launch choice. None = planner default; "native" = F.linear (keep_native).
+_CHOICES = {}
+_VALIDATED = {}
+#: Time candidate launch shapes at first use (eager only), as linear.py:436-481 does.
+TUNE = os.environ.get("FTK_TUNE", "0") == "1"
+
+
+def _as_rows(x):
+    rows = x.numel() // x.shape[-1]
+    return x.reshape(rows, x.shape[-1]).contiguous()
+
+
+def project(x, weight, config=None, out=None):
+    """y[M, N] = x[M, K] @ weight[N, K].T on the GPU (the device work of _project, linear.py:178-314).
+
+    ``config`` is a ``_native.Config`` (None = planner default). Raises on any
+    unsupported input; there is no fallback here.
+    """
+    _native.require_gpu(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("project takes BF16 x and weight")
+    if not weight.is_contiguous():
+        raise ValueError("project takes a contiguous [N, K] weight")
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError(f"x has K={k}, weight has K={weight.shape[1]}")
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    stream = _native.stream_of(x)
+    if config is None:
+        _native.call("ftk_linear_bf16", _native.ptr(x), _native.ptr(weight), _native.ptr(out), m, n, k, stream)
+    else:
+        _native.call("ftk_project_bf16", _native.ptr(x), None, 0.0, _native.ptr(weight), _native.ptr(out), m, n, k,
+                     _native.EPI_STORE, None, 0, None, None, 0, config, stream)
+    return out
+
+
+def rms_norm_linear(x, norm_weight, eps, weight, config=None):
+    """rms_norm(x, norm_weight, eps) @ weight.T with the norm folded into the projection's prologue.
+
+    Cast order of engine/kernels/rmsnorm.py:35-46 (normalised value rounded to
+    BF16 before the gain multiply). Shapes the fused kernel does not take
+    (K % 8 != 0, unaligned, M > 4) run the separate norm kernel, then ``linear``.
+    """
+    _native.require_gpu(x, norm_weight, weight)
+    shape = x.shape
+    flat = _as_rows(x)
+    m, k = flat.shape
+    n = weight.shape[0]
+    out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    status = _native.try_call(
+        "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
+        _native.ptr(out), m, n, k, _native.EPI_STORE, None, 0, None, None, 0, config, _native.stream_of(flat))
+    if status == _native.FTK_ERR_UNSUPPORTED:
+        from kernels.rmsnorm import rms_norm
+        return linear(rms_norm(x, norm_weight, eps), weight)
+    if status != _native.FTK_OK:
+        raise _native.FtkError("ftk_project_bf16", status)
+    return out.reshape(*shape[:-1], n)
+
+
+def _candidates(m, n, k):
+    """Launch shapes worth timing for one (M, N, K): planner default first."""
+    if m > 4 or k % 8:
+        return [None]
+    configs = [None]
+    for rpw, unroll in ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)):
+        for gpc in (4, 8):
+            configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc))
+    return configs
+
+
+def _time(fn, reps=20):
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        fn()
+    times = []
+    for _ in range(5):
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) / reps)
+    return statistics.median(times)
+
+
+def _agrees(x, weight, config, reference):
+    """Operator sanity check against the planner default (abs <= 0.016 |ref| + 0.001, linear.py:399-409)."""
+    got = project(x, weight, config).float()
+    ref = reference.float()
+    return bool(((got - ref).abs() <= ref.abs() * 0.016 + 0.001).all())
+
+
+def _choose(x, weight):
+    """Time the candidates once per shape, eagerly (linear.py:436-481); returns the fastest config."""
+    m, k = x.shape
+    n = weight.shape[0]
+    generator = torch.Generator(device=x.device).manual_seed(1729)
+    probe = torch.randn(x.shape, device=x.device, dtype=x.dtype, generator=generator)
+    reference = project(probe, weight)
+    validated = []
+    for config in _candidates(m, n, k):
+        if config is not None and not _agrees(probe, weight, config, reference):
+            continue
+        validated.append((_time(lambda: project(x, weight, config)), config))
+    validated.sort(key=lambda item: item[0])
+    _VALIDATED[(x.device, m, n, k)] = validated
+    return validated[0][1] if validated else None
+
+
+def keep_native(rows, weight):
+    """Leave a shape on torch's native GEMM without tuning it (linear.py:484-486)."""
+    _CHOICES.setdefault((weight.device, rows, weight.shape[0], weight.shape[1]), "native")
+
+
+def linear(x, weight, split_ok=False):
+    """x @ weight.T in BF16 (linear.py:489-523). ``split_ok`` is accepted; the result is always BF16."""
+    rows = x.numel() // x.shape[-1]
+    if rows > MAX_ROWS or x.dtype != torch.bfloat16 or not weight.is_contiguous():
+        return F.linear(x, weight)
+    _native.require_gpu(x, weight)
+    key = (x.device, rows, weight.shape[0], weight.shape[1])
+    if key not in _CHOICES:
+        if TUNE:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("projection selection must finish during eager warmup")
+            _CHOICES[key] = _choose(_as_rows(x), weight)
+            register(("projection",) + key[1:], rows, weight.shape[0] * weight.shape[1],
+                     [config for _, config in _VALIDATED.get(key, ())][:3],
+                     lambda: _CHOICES[key], lambda config: _CHOICES.__setitem__(key, config))
+        else:
+            _CHOICES[key] = None
+    choice = _CHOICES[key]
+    if choice == "native":
+        return F.linear(x, weight)
+    out = project(_as_rows(x), weight, choice)
+    return out.reshape(*x.shape[:-1], weight.shape[0])
+
+
+def plan(m, n, k, epilogue=_native.EPI_STORE, compute_units=256, config=None):
+    """The launch the C planner makes for a shape (host only; no device needed)."""
+    p = _native.Plan()
+    _native.call("ftk_plan_project", m, n, k, epilogue, compute_units, config, p)
+    return p

@@ -1,0 +1,165 @@
+/*
+ * ftk.h -- C ABI of the MI355X (gfx950) skinny BF16 projection library, libftk.so.
+ *
+ * The reference (john-jpet/fast-transformer) has no C ABI: its path is Python
+ * functions over Triton kernels (the .py files of engine/kernels/). Each entry point below
+ * replaces the device work under one of those functions; the Python package
+ * `kernels` (fast-transformer_amd/kernels/) keeps the reference's signatures and
+ * calls these through ctypes.
+ *
+ * Conventions
+ *   - Tensors are plain device pointers. BF16 is passed as raw 16-bit patterns.
+ *     Matrices are row-major: x[M, K], W[N, K] (PyTorch Linear layout, K
+ *     contiguous), y[M, N]. y = x @ W^T with FP32 accumulation and one
+ *     round-to-nearest-even to BF16 (engine/kernels/linear.py:1-6).
+ *   - `stream` is a hipStream_t (NULL = the null stream). Work is only
+ *     enqueued: nothing synchronizes, nothing allocates, so every entry point
+ *     can be captured into a hipGraph.
+ *   - Return value: FTK_OK or an ftk_status code. Nothing is launched when a
+ *     code other than FTK_OK or FTK_ERR_HIP is returned.
+ *   - M (rows of x) is 1..FTK_MAX_ROWS, as the reference's MAX_ROWS = 32
+ *     (engine/kernels/linear.py:343); larger M is the caller's native GEMM.
+ *   - Workspaces (argmax) must be zero-filled once when allocated; every
+ *     completed call leaves them zeroed. Calls that share a workspace must not
+ *     run concurrently.
+ */
+#ifndef FTK_H
+#define FTK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FTK_MAX_ROWS 32
+
+typedef enum ftk_status {
+  FTK_OK = 0,
+  FTK_ERR_INVALID = 1,      /* null pointer, non-positive size, M > FTK_MAX_ROWS, bad flag */
+  FTK_ERR_UNSUPPORTED = 2,  /* shape/alignment this fused entry point does not take (K % 8, 16-byte alignment) */
+  FTK_ERR_WORKSPACE = 3,    /* workspace missing or smaller than *_workspace_bytes() */
+  FTK_ERR_HIP = 4           /* the HIP launch failed; see ftk_last_hip_error() */
+} ftk_status;
+
+typedef enum ftk_epilogue {
+  FTK_EPI_STORE = 0,   /* y[m, n] = bf16(sum) */
+  FTK_EPI_SWIGLU = 1,  /* y[m, j] = bf16(bf16(silu(bf16(g_j))) * bf16(u_j)), W = cat(W_gate, W_up) */
+  FTK_EPI_ARGMAX = 2   /* logits (optional) + lowest-index greedy id per row */
+} ftk_epilogue;
+
+typedef enum ftk_kind {
+  FTK_KIND_AUTO = 0,
+  FTK_KIND_GEMV = 1,     /* M <= 4: HBM-streaming GEMV (v_dot2_f32_bf16, LDS-resident x) */
+  FTK_KIND_MFMA = 2,     /* M >= 4: v_mfma_f32_16x16x32_bf16 tiles */
+  FTK_KIND_GENERIC = 3   /* any shape/alignment, scalar loads; store epilogue only */
+} ftk_kind;
+
+/* Launch choice for one projection (the reference's per-shape config tuple,
+ * engine/kernels/linear.py:179 `kind, block_n, block_k, splits, warps`).
+ * Zero fields mean "planner default". */
+typedef struct ftk_config {
+  int kind;            /* ftk_kind */
+  int rows_per_wave;   /* GEMV: weight rows per wave per tile (2, 4, 8) */
+  int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4) */
+  int groups_per_cu;   /* grid cap = groups_per_cu * compute units (grid-stride beyond) */
+} ftk_config;
+
+typedef struct ftk_plan {
+  int kind;
+  int rows_per_wave;
+  int unroll;
+  int grid;            /* workgroups launched */
+  int tiles;           /* row tiles walked grid-stride */
+  int threads;         /* threads per workgroup */
+  int64_t lds_bytes;   /* dynamic LDS per workgroup */
+} ftk_plan;
+
+/* ---- library ------------------------------------------------------------- */
+const char* ftk_version(void);
+const char* ftk_status_string(int status);
+int ftk_last_hip_error(void);          /* hipError_t of the last FTK_ERR_HIP on this thread */
+int ftk_device_compute_units(void);    /* CUs of the current device, or -1 without a device */
+
+/* ---- projections ------------------------------------------------------------ */
+
+/* y = x @ W^T.  Replaces the device work of linear(x, weight, split_ok)
+ * (engine/kernels/linear.py:489-523) and _project (linear.py:178-314).
+ * Any N, K and alignment (unaligned or K % 8 != 0 takes the generic kind). */
+int ftk_linear_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* y = rms_norm(x, gamma, eps) @ W^T with the norm folded into the projection's
+ * prologue. Replaces rms_norm (engine/kernels/rmsnorm.py:49-72, cast order
+ * :35-46) followed by linear (layers.py:44 QKV). Needs K % 8 == 0, 16-byte
+ * aligned x, W, gamma (else FTK_ERR_UNSUPPORTED). */
+int ftk_rms_norm_linear_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M,
+                             int64_t N, int64_t K, void* stream);
+
+/* y[M, I] = swiglu(xn @ W^T) with W = cat(W_gate, W_up) [2I, K] and
+ * xn = rms_norm(x) when gamma != NULL (else x). Replaces linear(gate_up) +
+ * swiglu (engine/layers.py:99-102, engine/kernels/swiglu.py:13-40). */
+int ftk_gate_up_swiglu_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M,
+                            int64_t I, int64_t K, void* stream);
+
+/* Greedy ids of xn @ W^T (xn = rms_norm(x) when gamma != NULL), lowest index
+ * on ties of the BF16-rounded logits; logits [M, V] written when non-NULL,
+ * top[M] = winning logit (FP32) when non-NULL; ids are int32 (ids_bytes 4) or
+ * int64 (8). Replaces the final norm + lm_head linear + argmax
+ * (engine/decode.py:274-278, engine/kernels/argmax.py:51-70, fused_argmax
+ * argmax.py:112-129, greedy_tokens argmax.py:132-167). */
+int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const void* w, void* logits, void* ids,
+                            int ids_bytes, float* top, int64_t M, int64_t V, int64_t K, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/* General form of the three above with an explicit launch choice (cfg may be
+ * NULL): the tuner's entry point (engine/kernels/linear.py:436-481 _choose). */
+int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M, int64_t N,
+                     int64_t K, int epilogue, void* ids, int ids_bytes, float* top, void* workspace,
+                     int64_t workspace_bytes, const ftk_config* cfg, void* stream);
+
+/* ---- standalone operators ---------------------------------------------------- */
+
+/* rms_norm(x, weight, eps) (engine/kernels/rmsnorm.py:49-72): x rows of
+ * `row_stride` elements, y contiguous [rows, cols]. */
+int ftk_rms_norm_bf16(const void* x, int64_t row_stride, const void* gamma, void* y, int64_t rows, int64_t cols,
+                      float eps, void* stream);
+
+/* add_rms_norm(x, residual, weight, eps) (engine/kernels/rmsnorm.py:98-125):
+ * x is BF16 [rows, cols] (x_splits = 0) or the FP32 partials of a Split
+ * [x_splits, rows*cols] with split stride x_split_stride elements
+ * (engine/kernels/merged.py:13-45). Writes y (normalized) and sum (BF16 x + r). */
+int ftk_add_rms_norm_bf16(const void* x, int x_splits, int64_t x_split_stride, const void* residual,
+                          const void* gamma, void* y, void* sum, int64_t rows, int64_t cols, float eps, void* stream);
+
+/* swiglu(packed) (engine/kernels/swiglu.py:27-40): packed [rows, 2*width] BF16
+ * (splits = 0) or FP32 split partials; out [rows, width]. */
+int ftk_swiglu_bf16(const void* packed, int splits, int64_t split_stride, void* out, int64_t rows, int64_t width,
+                    void* stream);
+
+/* argmax(logits, top=) (engine/kernels/argmax.py:51-70): BF16 logits [rows, vocab]. */
+int ftk_argmax_bf16(const void* logits, int64_t rows, int64_t vocab, void* ids, int ids_bytes, float* top,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* bf16(sum of FP32 split partials) (engine/kernels/linear.py:81-93 _merge_projection). */
+int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream);
+
+/* Workspace bytes of the argmax entry points for `rows` rows. */
+int64_t ftk_argmax_workspace_bytes(int64_t rows);
+
+/* ---- planning (host only, no device needed) ---------------------------------- */
+
+/* The launch ftk_project_bf16 would make for this shape on `compute_units` CUs. */
+int ftk_plan_project(int64_t M, int64_t N, int64_t K, int epilogue, int compute_units, const ftk_config* cfg,
+                     ftk_plan* plan);
+
+/* Replays `plan`'s tile walk on the host with the kernels' own index functions:
+ * counts[c] = number of (workgroup, tile, wave, slot) writing output column c
+ * (length outputs = N, or N/2 for SwiGLU); *max_row = largest weight row read. */
+int ftk_plan_coverage(const ftk_plan* plan, int64_t N, int epilogue, int32_t* counts, int64_t outputs,
+                      int64_t* max_row);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FTK_H */

@@ -1,0 +1,113 @@
+"""CPU-side checks of libftk.so: it loads, exports every entry point of include/ftk.h,
+validates arguments before touching a device, and its launch plans cover every
+output exactly once with in-bounds weight rows (replayed with the kernels' own
+index functions). No kernel runs here."""
+
+import ctypes
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+from kernels import _native
+
+HEADER = ROOT / "include" / "ftk.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(ftk_\w+)\(", text, re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    names = declared()
+    assert len(names) >= 15
+    lib = _native.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    # and nm agrees: every declared name is a dynamic text symbol
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (ftk_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_binding_signatures_cover_header():
+    assert set(declared()) == set(_native.SIGNATURES)
+
+
+def test_version_and_status_strings():
+    lib = _native.lib()
+    assert b"gfx950" in lib.ftk_version()
+    for code in range(5):
+        assert lib.ftk_status_string(code)
+    assert lib.ftk_argmax_workspace_bytes(1) == 16
+    assert lib.ftk_argmax_workspace_bytes(32) == 8 * 32 + 8
+
+
+def test_invalid_arguments_rejected_before_any_launch():
+    lib = _native.lib()
+    assert lib.ftk_linear_bf16(None, None, None, 1, 8, 8, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_rms_norm_linear_bf16(None, None, 1e-6, None, None, 1, 8, 8, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_rms_norm_bf16(None, 8, None, None, 1, 8, 1e-6, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_swiglu_bf16(None, 0, 0, None, 1, 8, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_merge_splits_bf16(None, 1, 8, None, None) == _native.FTK_ERR_INVALID
+    fake = ctypes.c_void_p(16)
+    # argmax without a workspace
+    assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 8, None, None, 0, None) == _native.FTK_ERR_WORKSPACE
+    assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 3, None, fake, 64, None) == _native.FTK_ERR_INVALID
+
+
+@pytest.mark.parametrize("m", [0, 33])
+def test_rows_outside_one_to_max_rows_rejected(m):
+    p = _native.Plan()
+    assert _native.lib().ftk_plan_project(m, 64, 64, 0, 256, None, p) == _native.FTK_ERR_INVALID
+
+
+SHAPES = [
+    # Qwen3-0.6B and Qwen3-8B projections (N, K) plus lm_head, and the reference's ragged test shapes
+    (4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072),
+    (6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288), (151936, 4096),
+    (200, 300), (130, 517), (173, 259), (257, 512), (127, 256), (70, 264),
+]
+
+
+def _coverage(plan, n, epilogue):
+    outputs = n // 2 if epilogue == _native.EPI_SWIGLU else n
+    counts = (ctypes.c_int32 * outputs)()
+    max_row = ctypes.c_int64()
+    _native.call("ftk_plan_coverage", plan, n, epilogue, counts, outputs, ctypes.byref(max_row))
+    return np.frombuffer(counts, dtype=np.int32), max_row.value
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_plan_writes_every_output_once(m, n, k):
+    for epilogue in (_native.EPI_STORE, _native.EPI_SWIGLU, _native.EPI_ARGMAX):
+        if epilogue == _native.EPI_SWIGLU and n % 2:
+            continue
+        for cfg in [None] + [_native.Config(0, rpw, u, gpc) for rpw, u in ((2, 4), (4, 2), (8, 1)) for gpc in (1, 8)]:
+            if cfg is not None and k % 8:
+                continue
+            p = _native.Plan()
+            status = _native.lib().ftk_plan_project(m, n, k, epilogue, 256, cfg, p)
+            if k % 8 and epilogue != _native.EPI_STORE:
+                assert status == _native.FTK_ERR_UNSUPPORTED
+                continue
+            assert status == _native.FTK_OK, (m, n, k, epilogue, cfg)
+            counts, max_row = _coverage(p, n, epilogue)
+            assert np.all(counts == 1), (m, n, k, epilogue, cfg)
+            assert max_row == n - 1
+            assert p.grid >= 1 and p.grid <= max(p.tiles, 1)
+            if p.kind == _native.KIND_GEMV:
+                assert p.lds_bytes == m * k * 2
+
+
+def test_plan_kinds():
+    p = _native.Plan()
+    _native.call("ftk_plan_project", 1, 4096, 4096, 0, 256, None, p)
+    assert p.kind == _native.KIND_GEMV and p.threads == 256
+    _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
+    assert p.kind == _native.KIND_GENERIC
