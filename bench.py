@@ -1,0 +1,367 @@
+"""Benchmark of the decode-time skinny BF16 projection path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-shapes]
+
+One step = one M=1 decode step's projections at Qwen3-8B shapes (BASELINE
+config 3): 36 layers, each RMSNorm-prologue QKV 4096->6144, O 4096->4096,
+RMSNorm-prologue gate/up 4096->2x12288 with the SwiGLU epilogue, down
+12288->4096, every layer with its own weights (13.9 GB resident in HBM), then
+the final RMSNorm + lm_head 4096->151936 + greedy argmax (1.24 GB). Weights and
+inputs are synthetic (seed 0; W ~ N(0, 0.02), x ~ N(0, 1), gamma ~ 1 + N(0, 0.1)).
+The step is captured once into a graph and replayed; the timed region is K
+replays bracketed by device synchronizations.
+
+value = algorithmic bytes of the step / step time (GB/s). Rank 0 prints one
+JSON line with the contract fields plus ``roofline`` (dominant kernel: the
+fused gate/up + SwiGLU GEMV), ``cpu_baseline`` (the reference's torch CPU path on
+a bounded sample of the same workload) and ``per_shape`` (µs, GB/s and fraction
+of the 8 TB/s HBM roofline for every BASELINE configuration).
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "fast-transformer_amd"))
+
+from kernels import _native  # noqa: E402
+from kernels import argmax as A  # noqa: E402
+from kernels import linear as L  # noqa: E402
+from kernels import swiglu as S  # noqa: E402
+
+METRIC = "M=1 bf16 GEMV HBM GB/s (% of peak) + µs/decode-layer, Qwen3-8B shapes"
+PEAK_GBS = 8000.0          # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # dense BF16 MFMA
+EPS = 1e-6
+
+QWEN3_8B = dict(hidden=4096, inter=12288, q_heads=32, kv_heads=8, head_dim=128, layers=36, vocab=151936)
+QWEN3_06B = dict(hidden=1024, inter=3072, q_heads=16, kv_heads=8, head_dim=128, layers=28, vocab=151936)
+
+
+def layer_bytes(cfg, m):
+    """Algorithmic bytes of one layer's projection set (2NK + 2MK + 2MN_out, + 2K per norm gain)."""
+    h, i = cfg["hidden"], cfg["inter"]
+    q = cfg["q_heads"] * cfg["head_dim"]
+    qkv_n = q + 2 * cfg["kv_heads"] * cfg["head_dim"]
+    qkv = 2 * qkv_n * h + 2 * m * h + 2 * m * qkv_n + 2 * h
+    o = 2 * h * q + 2 * m * q + 2 * m * h
+    gate_up = 2 * 2 * i * h + 2 * m * h + 2 * m * i + 2 * h
+    down = 2 * h * i + 2 * m * i + 2 * m * h
+    return {"qkv": qkv, "o": o, "gate_up": gate_up, "down": down}
+
+
+def head_bytes(cfg, m):
+    h, v = cfg["hidden"], cfg["vocab"]
+    return 2 * v * h + 2 * m * h + 2 * m * v + 2 * h + 4 * m
+
+
+class Model:
+    """Synthetic random-init weights of one model's projection path, resident on the GPU."""
+
+    def __init__(self, cfg, device, layers=None, head=True, seed=0):
+        self.cfg = cfg
+        g = torch.Generator(device=device).manual_seed(seed)
+        h, i = cfg["hidden"], cfg["inter"]
+        q = cfg["q_heads"] * cfg["head_dim"]
+        qkv_n = q + 2 * cfg["kv_heads"] * cfg["head_dim"]
+
+        def w(n, k):
+            return (torch.randn((n, k), generator=g, device=device) * 0.02).to(torch.bfloat16)
+
+        def gamma(k):
+            return (1 + 0.1 * torch.randn((k,), generator=g, device=device)).to(torch.bfloat16)
+
+        self.layers = []
+        for _ in range(cfg["layers"] if layers is None else layers):
+            self.layers.append(dict(qkv=w(qkv_n, h), o=w(h, q), gate_up=w(2 * i, h), down=w(h, i)))
+        for layer in self.layers:
+            layer["ln1"], layer["ln2"] = gamma(h), gamma(h)
+        self.head = w(cfg["vocab"], h) if head else None
+        self.final_norm = gamma(h)
+        self.q = q
+
+
+class Step:
+    """The decode step's projection path at M rows, with its input/output buffers preallocated."""
+
+    def __init__(self, model, m, device, seed=1):
+        self.model, self.m = model, m
+        cfg = model.cfg
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.h = torch.randn((m, cfg["hidden"]), generator=g, device=device).to(torch.bfloat16)
+        # attention output feeding O: attention itself is outside the path
+        self.attn = torch.randn((m, model.q), generator=g, device=device).to(torch.bfloat16)
+        self.top = torch.empty(m, dtype=torch.float32, device=device)
+
+    def layer(self, lw, h):
+        qkv = L.rms_norm_linear(h, lw["ln1"], EPS, lw["qkv"])
+        o = L.linear(self.attn, lw["o"])
+        act = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS)
+        return qkv, L.linear(act, lw["down"])
+
+    def layers(self):
+        h = self.h
+        for lw in self.model.layers:
+            _, h = self.layer(lw, h)
+        return h
+
+    def run(self):
+        h = self.layers()
+        return A.lm_head_argmax(h, self.model.head, self.model.final_norm, EPS, logits=True, top=self.top)
+
+
+def capture(fn, warm=2):
+    """Warm ``fn`` eagerly (selection, workspaces), then capture it into a graph on a side stream."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, reps=10, inner=1):
+    """Median wall time of one replay, from HIP events on the replay stream (µs)."""
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(reps):
+        start.record()
+        for _ in range(inner):
+            graph.replay()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e3 / inner)
+    return statistics.median(times)
+
+
+def shape_entry(us, byts, flops=None):
+    e = {"us": round(us, 3), "GB_s": round(byts / us / 1e3, 1), "frac_hbm": round(byts / us / 1e3 / PEAK_GBS, 4),
+         "bytes": int(byts)}
+    if flops is not None:
+        e["mfma_util"] = round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 5)
+    return e
+
+
+def per_kind(step, kind):
+    """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch."""
+    def fn():
+        for lw in step.model.layers:
+            if kind == "qkv":
+                L.rms_norm_linear(step.h, lw["ln1"], EPS, lw["qkv"])
+            elif kind == "o":
+                L.linear(step.attn, lw["o"])
+            elif kind == "gate_up":
+                S.gate_up_swiglu(step.h, lw["gate_up"], lw["ln2"], EPS)
+            else:
+                L.linear(step.act_in, lw["down"])
+    if kind == "down":
+        step.act_in = torch.randn((step.m, step.model.cfg["inter"]), device=step.h.device).to(torch.bfloat16)
+    graph = capture(fn)
+    return time_graph(graph) / len(step.model.layers)
+
+
+def cpu_baseline(model, step, budget_s):
+    """The reference's torch-CPU path (BF16 F.linear + native-cast norm/SwiGLU) on a bounded sample.
+
+    Sample: the first two of the 36 layers at M=1, repeated until ~budget_s of CPU work.
+    """
+    from oracle import torch_cpu
+
+    threads = torch.get_num_threads()  # the host's CPU share (OMP_NUM_THREADS)
+    layers = [{k: v.cpu() for k, v in model.layers[i].items()} for i in range(2)]
+    h, attn = step.h.cpu(), step.attn.cpu()
+    torch_cpu.layer_projections(h, attn, layers[0], EPS)  # warm
+    times, t_end = [], time.monotonic() + budget_s
+    while time.monotonic() < t_end and len(times) < 50:
+        t0 = time.perf_counter()
+        for lw in layers:
+            torch_cpu.layer_projections(h, attn, lw, EPS)
+        times.append((time.perf_counter() - t0) / len(layers))
+    us = statistics.median(times) * 1e6
+    byts = sum(layer_bytes(model.cfg, 1).values())
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(byts / us / 1e3, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"2 of 36 Qwen3-8B-shape layers at M=1 (QKV+O+gate/up+SwiGLU+down, torch CPU BF16), "
+                      f"median of {len(times)} passes; {us:.0f} us/layer; CPU: {cpu_model}",
+            "us_per_layer": round(us, 1)}
+
+
+def load_traffic():
+    f = ROOT / "profiles" / "traffic_gate_up_swiglu_8b_m1.json"
+    if f.exists():
+        return json.loads(f.read_text()).get("traffic_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-configuration table")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--profile-gate-up", type=int, default=0, metavar="PASSES",
+                    help="profiling mode: only PASSES eager passes of the 36 gate/up + SwiGLU launches, "
+                         "then one 1 GiB device copy as the counter reference")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this path has no multi-GPU form in this build "
+              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    props = torch.cuda.get_device_properties(dev)
+    _native.lib()
+
+    cfg = QWEN3_8B
+    if args.profile_gate_up:
+        profile_gate_up(cfg, dev, args.profile_gate_up)
+        return
+    model = Model(cfg, dev)
+    step = Step(model, 1, dev)
+    graph = capture(step.run)
+    layer_graph = capture(step.layers)
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    lb = layer_bytes(cfg, 1)
+    step_bytes = cfg["layers"] * sum(lb.values()) + head_bytes(cfg, 1)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    us_layers = time_graph(layer_graph, reps=10)
+    us_per_layer = us_layers / cfg["layers"]
+    layer_lb_us = sum(lb.values()) / (PEAK_GBS * 1e3)
+
+    # dominant kernel: the fused gate/up + SwiGLU GEMV (201 MB per launch at M=1)
+    gu_us = per_kind(step, "gate_up")
+    gu_bytes = lb["gate_up"]
+    roofline = {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
+                "kernel": "gemv_kernel<1,RPW,U,PRO=1,SWIGLU> (Qwen3-8B gate/up 4096->2x12288, M=1)",
+                "avg_launch_us": round(gu_us, 3)}
+
+    per_shape = {}
+    if not args.no_shapes:
+        per_shape = shapes_table(model, step, dev)
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "Qwen3-8B-shape decode projections, M=1: 36 layers (RMSNorm-prologue QKV, O, "
+                               "RMSNorm-prologue gate/up + SwiGLU, down) + final RMSNorm + lm_head + argmax",
+                   "rows": 1, "layers": cfg["layers"], "hidden": cfg["hidden"], "intermediate": cfg["inter"],
+                   "vocab": cfg["vocab"], "weights_gb": round(step_bytes / 1e9, 2), "graph": True,
+                   "parallelism": "single GPU"},
+        "frac_peak": round(value / PEAK_GBS, 4),
+        "us_per_layer": round(us_per_layer, 2), "layer_lower_bound_us": round(layer_lb_us, 2),
+        "layer_vs_bound": round(us_per_layer / layer_lb_us, 3),
+        "roofline": roofline,
+        "device": {"name": props.name, "cus": props.multi_processor_count},
+    }
+    if per_shape:
+        result["per_shape"] = per_shape
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(model, step, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def profile_gate_up(cfg, dev, passes):
+    """Eager launches of the dominant kernel only (for rocprofv3 counter runs), plus a copy of known size."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    h, i = cfg["hidden"], cfg["inter"]
+    weights = [(torch.randn((2 * i, h), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+               for _ in range(cfg["layers"])]
+    gamma = (1 + 0.1 * torch.randn((h,), generator=g, device=dev)).to(torch.bfloat16)
+    x = torch.randn((1, h), generator=g, device=dev).to(torch.bfloat16)
+    for p in range(passes):
+        for w in weights:
+            S.gate_up_swiglu(x, w, gamma, EPS)
+        torch.cuda.synchronize()
+        print(f"profile pass {p + 1}/{passes} done", flush=True)
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # reference kernel: reads and writes exactly 1 GiB
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "profile-gate-up", "passes": passes, "launches": passes * cfg["layers"],
+                      "bytes_per_launch": layer_bytes(cfg, 1)["gate_up"], "copy_bytes": 1 << 30}), flush=True)
+
+
+def shapes_table(model8, step8, dev):
+    """µs / GB/s / fraction of the HBM roofline for every BASELINE configuration (C1-C5)."""
+    out = {}
+    cfg = model8.cfg
+    lb = layer_bytes(cfg, 1)
+    for kind in ("qkv", "o", "gate_up", "down"):
+        us = per_kind(step8, kind)
+        out[f"C3 8B {kind} M=1"] = shape_entry(us, lb[kind])
+    # C5: lm_head + argmax at M=1 and M=5
+    for m in (1, 5):
+        st = step8 if m == 1 else Step(model8, m, dev, seed=5)
+        h = torch.randn((m, cfg["hidden"]), device=dev).to(torch.bfloat16)
+        g = capture(lambda: A.lm_head_argmax(h, model8.head, model8.final_norm, EPS, logits=True, top=st.top))
+        us = time_graph(g)
+        out[f"C5 lm_head+argmax M={m}"] = shape_entry(us, head_bytes(cfg, m), 2 * m * cfg["vocab"] * cfg["hidden"])
+    # C4: 8B layer set at M = 5, 8, 16
+    for m in (5, 8, 16):
+        st = Step(model8, m, dev, seed=m)
+        g = capture(st.layers)
+        us = time_graph(g, reps=5) / cfg["layers"]
+        byts = sum(layer_bytes(cfg, m).values())
+        flops = 2 * m * sum(n * k for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)))
+        out[f"C4 8B layer M={m}"] = shape_entry(us, byts, flops)
+    # C3 per layer (M=1)
+    g = capture(step8.layers)
+    us = time_graph(g, reps=5) / cfg["layers"]
+    out["C3 8B layer M=1"] = shape_entry(us, sum(lb.values()))
+    # C1 / C2: Qwen3-0.6B shapes
+    model06 = Model(QWEN3_06B, dev, head=False, seed=2)
+    st06 = Step(model06, 1, dev, seed=3)
+    g = capture(st06.layers)
+    us = time_graph(g, reps=10) / QWEN3_06B["layers"]
+    out["C2 0.6B layer M=1"] = shape_entry(us, sum(layer_bytes(QWEN3_06B, 1).values()))
+    x = torch.randn((1, 1024), device=dev).to(torch.bfloat16)
+    copies = [torch.randn((4096, 1024), device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(64)]
+    ys = [torch.empty((1, 4096), device=dev, dtype=torch.bfloat16) for _ in range(64)]
+    g = capture(lambda: [L.project(x, w, out=y) for w, y in zip(copies, ys)])
+    us = time_graph(g) / 64
+    out["C1 0.6B qkv M=1 (no prologue)"] = shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096)
+    del model06, copies
+    return out
+
+
+if __name__ == "__main__":
+    main()

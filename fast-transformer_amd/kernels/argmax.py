@@ -42,8 +42,8 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
                    config=None):
     """(ids, logits or None): greedy ids of rms_norm?(x) @ weight.T in one projection kernel.
 
-    Ties go to the lowest index of the BF16-rounded logits. Returns None for
-    shapes the fused kernel does not take (the caller then projects and calls ``argmax``).
+    Ties go to the lowest index of the BF16-rounded logits. Shapes the fused
+    kernel does not take run the norm, projection and argmax kernels in turn.
     """
     _native.require_gpu(x, weight, norm_weight, top)
     shape = x.shape
@@ -59,10 +59,21 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
         _native.ptr(out), m, v, k, _native.EPI_ARGMAX, _native.ptr(ids), ids_bytes, _native.ptr(top),
         _native.ptr(ws), ws.numel(), config, _native.stream_of(flat))
     if status == _native.FTK_ERR_UNSUPPORTED:
-        return None
+        from kernels.linear import linear
+        from kernels.rmsnorm import rms_norm
+
+        xn = x if norm_weight is None else rms_norm(x, norm_weight, eps)
+        full = linear(xn, weight)
+        return argmax(full, top=top).to(ids_dtype), (full if logits else None)
     if status != _native.FTK_OK:
         raise _native.FtkError("ftk_project_bf16", status)
     return ids, out
+
+
+def fused_applies(rows, k, n):
+    """Whether the fused lm_head + argmax kernel takes this shape."""
+    p = _native.Plan()
+    return _native.lib().ftk_plan_project(rows, n, k, _native.EPI_ARGMAX, 256, None, p) == _native.FTK_OK
 
 
 def fused_argmax(x, weight, block_n=64, block_k=128):
@@ -74,8 +85,9 @@ def fused_argmax(x, weight, block_n=64, block_k=128):
     rows = x.numel() // x.shape[-1]
     if rows > _native.MAX_ROWS or x.dtype != torch.bfloat16 or not weight.is_contiguous():
         return None
-    result = lm_head_argmax(x, weight, logits=False)
-    return None if result is None else result[0]
+    if not fused_applies(rows, x.shape[-1], weight.shape[0]):
+        return None
+    return lm_head_argmax(x, weight, logits=False)[0]
 
 
 def greedy_tokens(x, weight, linear, top=None):
@@ -89,10 +101,8 @@ def greedy_tokens(x, weight, linear, top=None):
     from kernels import linear as _linear_module
 
     if linear is _linear_module.linear:
-        result = lm_head_argmax(x, weight, logits=top is not None, top=top)
-        if result is not None:
-            ids, logits = result
-            return (ids, logits) if top is not None else ids
+        ids, logits = lm_head_argmax(x, weight, logits=top is not None, top=top)
+        return (ids, logits) if top is not None else ids
     logits = linear(x, weight)
     if top is not None:
         return argmax(logits, top=top), logits
