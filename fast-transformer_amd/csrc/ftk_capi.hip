@@ -35,10 +35,14 @@ DeviceInfo device_info() {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Planner defaults for the GEMV kind.
-constexpr int kDefaultRpw = 4;
-constexpr int kDefaultUnroll = 2;
+// Planner defaults (from the launch-shape sweeps on MI355X).
+constexpr int kDefaultRpw = 2;
+constexpr int kDefaultUnroll = 4;
 constexpr int kDefaultGroupsPerCu = 8;
+constexpr int kMfmaDefaultUnroll = 4;
+constexpr int kMfmaDefaultWaves = 16;
+
+static int64_t argmax_keys_bytes(int grid, int64_t M) { return kWsKeys + (int64_t)grid * M * 8; }
 
 static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_config* cfg, ftk_plan* p) {
   memset(p, 0, sizeof(*p));
@@ -47,9 +51,11 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (epi < FTK_EPI_STORE || epi > FTK_EPI_ARGMAX) return FTK_ERR_INVALID;
   if (epi == FTK_EPI_SWIGLU && (N % 2)) return FTK_ERR_INVALID;
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
-  if (kind == FTK_KIND_AUTO) kind = (K % 8 == 0 && M <= 4) ? FTK_KIND_GEMV : FTK_KIND_GENERIC;
+  if (kind == FTK_KIND_AUTO) kind = K % 8 ? FTK_KIND_GENERIC : M <= 4 ? FTK_KIND_GEMV : FTK_KIND_MFMA;
   p->kind = kind;
   p->threads = kThreads;
+  p->splits = 1;
+  p->k_slice = (int)K;
   if (kind == FTK_KIND_GENERIC) {
     if (epi != FTK_EPI_STORE) return FTK_ERR_UNSUPPORTED;
     p->tiles = (int)((N + kWaves - 1) / kWaves);
@@ -58,8 +64,9 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->unroll = 1;
     return FTK_OK;
   }
+  if (K % 8 != 0) return FTK_ERR_UNSUPPORTED;
   if (kind == FTK_KIND_GEMV) {
-    if (K % 8 != 0 || M > 4) return FTK_ERR_UNSUPPORTED;
+    if (M > 4) return FTK_ERR_UNSUPPORTED;
     const int rpw = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : kDefaultRpw;
     const int unroll = cfg && cfg->unroll ? cfg->unroll : kDefaultUnroll;
     const int gpc = cfg && cfg->groups_per_cu ? cfg->groups_per_cu : kDefaultGroupsPerCu;
@@ -71,10 +78,35 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     const int64_t cap = (int64_t)gpc * cus;
     p->grid = (int)(p->tiles < cap ? p->tiles : cap);
     p->lds_bytes = M * K * 2;
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     if (p->lds_bytes > 160 * 1024) return FTK_ERR_UNSUPPORTED;
     return FTK_OK;
   }
-  return FTK_ERR_UNSUPPORTED;
+  if (kind == FTK_KIND_MFMA) {
+    // Defaults from the MI355X sweep: 16 rows (SwiGLU: one gate + one up subtile)
+    // per workgroup of 16 waves; 32 rows once M > 16 (two MFMA column blocks).
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : (epi == FTK_EPI_SWIGLU || M > 16 ? 32 : 16);
+    if (rows % 16) return FTK_ERR_INVALID;
+    const int t = rows / 16;
+    const int unroll = cfg && cfg->unroll ? cfg->unroll : (t >= 4 ? 2 : kMfmaDefaultUnroll);
+    const int waves = cfg && cfg->waves ? cfg->waves : (epi == FTK_EPI_SWIGLU ? 8 : kMfmaDefaultWaves);
+    if (!mfma_supported((int)M, t, unroll, waves, epi)) return FTK_ERR_INVALID;
+    p->rows_per_wave = rows;
+    p->unroll = unroll;
+    p->threads = 64 * waves;
+    p->tiles = mfma_tiles(epi, (int)N, t);
+    p->grid = p->tiles;
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : kWsKeys;  // row scales
+    return FTK_OK;
+  }
+  return FTK_ERR_INVALID;
+}
+
+// Workspace a call needs: argmax keys, and the RMSNorm row scales of the MFMA kind.
+static int64_t call_workspace(const ftk_plan& p, int epi, bool pro) {
+  if (epi == FTK_EPI_ARGMAX) return p.workspace_bytes;
+  if (p.kind == FTK_KIND_MFMA && pro) return kWsKeys;
+  return 0;
 }
 
 }  // namespace ftk
@@ -103,12 +135,22 @@ int ftk_device_compute_units(void) {
   return d.ok ? d.cus : -1;
 }
 
-int64_t ftk_argmax_workspace_bytes(int64_t rows) { return rows < 1 ? 0 : 8 * rows + 8; }
+int64_t ftk_argmax_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows < 1 || vocab < 1 || vocab > INT32_MAX) return 0;
+  return 8 * rows * argmax_blocks((int)vocab);
+}
 
 int ftk_plan_project(int64_t M, int64_t N, int64_t K, int epilogue, int compute_units, const ftk_config* cfg,
                      ftk_plan* p) {
   if (p == nullptr) return FTK_ERR_INVALID;
   return plan(M, N, K, epilogue, compute_units, cfg, p);
+}
+
+int64_t ftk_project_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue, const ftk_config* cfg) {
+  DeviceInfo d = device_info();
+  ftk_plan p;
+  if (plan(M, N, K, epilogue, d.ok ? d.cus : 256, cfg, &p) != FTK_OK) return 0;
+  return p.workspace_bytes;
 }
 
 int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* counts, int64_t outputs,
@@ -126,6 +168,24 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
           if (row > *max_row) *max_row = row;
         }
       }
+    return FTK_OK;
+  }
+  if (p->kind == FTK_KIND_MFMA) {
+    // Workgroup b owns tile b: T subtiles of 16 weight rows over all of K.
+    const int t = p->rows_per_wave / 16;
+    if (t < 1 || p->grid != p->tiles) return FTK_ERR_INVALID;
+    const int per = mfma_out_per_tile(epilogue, t);
+    for (int b = 0; b < p->grid; ++b) {
+      for (int sub = 0; sub < t; ++sub)
+        for (int li = 0; li < 16; ++li) {
+          const int64_t row = mfma_weight_row(epilogue, b, sub, li, (int)N, t);
+          if (row > *max_row) *max_row = row;
+        }
+      for (int r = 0; r < per; ++r) {
+        const int64_t col = (int64_t)b * per + r;
+        if (col < outputs) counts[col] += 1;
+      }
+    }
     return FTK_OK;
   }
   if (p->kind != FTK_KIND_GEMV) return FTK_ERR_UNSUPPORTED;
@@ -153,13 +213,15 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   if (epilogue != FTK_EPI_ARGMAX && y == nullptr) return FTK_ERR_INVALID;
   if (epilogue == FTK_EPI_ARGMAX) {
     if (ids == nullptr || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
-    if (workspace == nullptr || workspace_bytes < ftk_argmax_workspace_bytes(M)) return FTK_ERR_WORKSPACE;
+    if (workspace == nullptr) return FTK_ERR_WORKSPACE;
   }
   DeviceInfo d = device_info();
   if (!d.ok) return hip_status(hipErrorNoDevice);
   ftk_plan p;
   int st = plan(M, N, K, epilogue, d.cus, cfg, &p);
   if (st != FTK_OK) return st;
+  const int64_t need = call_workspace(p, epilogue, gamma != nullptr);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return FTK_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (p.kind == FTK_KIND_GENERIC) {
     if (gamma != nullptr) return FTK_ERR_UNSUPPORTED;
@@ -180,35 +242,50 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   a.ids = ids;
   a.ids_bytes = ids_bytes;
   a.top = top;
-  if (epilogue == FTK_EPI_ARGMAX) {
-    a.keys = (unsigned long long*)workspace;
-    a.ticket = (unsigned int*)((char*)workspace + 8 * M);
+  char* ws = (char*)workspace;
+  if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
+  hipError_t e;
+  if (p.kind == FTK_KIND_GEMV) {
+    GemvShape g = {p.rows_per_wave, p.unroll, p.grid, p.tiles, (size_t)p.lds_bytes};
+    e = launch_gemv(a, epilogue, g, s);
+  } else {
+    MfmaShape shape = {p.rows_per_wave / 16, p.unroll, p.threads / 64, p.grid};
+    MfmaArgs m;
+    m.row_scale = gamma != nullptr ? (const float*)(ws + kWsScale) : nullptr;
+    e = launch_mfma(a, epilogue, shape, m, s);
   }
-  GemvShape g = {p.rows_per_wave, p.unroll, p.grid, p.tiles, (size_t)p.lds_bytes};
-  return hip_status(launch_gemv(a, epilogue, g, s));
+  if (e == hipSuccess && epilogue == FTK_EPI_ARGMAX)
+    e = launch_argmax_finalize(a.keys, p.grid, (int)M, ids, ids_bytes, top, s);
+  return hip_status(e);
 }
 
 int ftk_linear_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
   if (x && w && (!aligned16(x) || !aligned16(w))) {
-    ftk_config c = {FTK_KIND_GENERIC, 0, 0, 0};
+    ftk_config c = {FTK_KIND_GENERIC, 0, 0, 0, 0};
     return ftk_project_bf16(x, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, &c,
                             stream);
   }
-  return ftk_project_bf16(x, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, nullptr,
-                          stream);
+  const int st = ftk_project_bf16(x, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0,
+                                 nullptr, stream);
+  if (st == FTK_ERR_UNSUPPORTED) {  // e.g. an unsplit MFMA x slice larger than LDS: no workspace here
+    ftk_config c = {FTK_KIND_GENERIC, 0, 0, 0, 0};
+    return ftk_project_bf16(x, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, &c,
+                            stream);
+  }
+  return st;
 }
 
 int ftk_rms_norm_linear_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M,
                              int64_t N, int64_t K, void* stream) {
   if (gamma == nullptr) return FTK_ERR_INVALID;
-  if (K % 8 || M > 4) return FTK_ERR_UNSUPPORTED;
+  if (K % 8) return FTK_ERR_UNSUPPORTED;
   return ftk_project_bf16(x, gamma, eps, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, nullptr,
                           stream);
 }
 
 int ftk_gate_up_swiglu_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M,
                             int64_t I, int64_t K, void* stream) {
-  if (K % 8 || M > 4) return FTK_ERR_UNSUPPORTED;
+  if (K % 8) return FTK_ERR_UNSUPPORTED;
   return ftk_project_bf16(x, gamma, eps, w, y, M, 2 * I, K, FTK_EPI_SWIGLU, nullptr, 0, nullptr, nullptr, 0,
                           nullptr, stream);
 }
@@ -216,7 +293,7 @@ int ftk_gate_up_swiglu_bf16(const void* x, const void* gamma, float eps, const v
 int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const void* w, void* logits, void* ids,
                             int ids_bytes, float* top, int64_t M, int64_t V, int64_t K, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-  if (K % 8 || M > 4) return FTK_ERR_UNSUPPORTED;
+  if (K % 8) return FTK_ERR_UNSUPPORTED;
   return ftk_project_bf16(x, gamma, eps, w, logits, M, V, K, FTK_EPI_ARGMAX, ids, ids_bytes, top, workspace,
                           workspace_bytes, nullptr, stream);
 }
@@ -254,11 +331,9 @@ int ftk_argmax_bf16(const void* logits, int64_t rows, int64_t vocab, void* ids, 
                     void* workspace, int64_t workspace_bytes, void* stream) {
   if (!logits || !ids || rows < 1 || vocab < 1 || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
   if (rows > 65535 || vocab > INT32_MAX) return FTK_ERR_INVALID;
-  if (workspace == nullptr || workspace_bytes < ftk_argmax_workspace_bytes(rows)) return FTK_ERR_WORKSPACE;
-  unsigned long long* keys = (unsigned long long*)workspace;
-  unsigned int* ticket = (unsigned int*)((char*)workspace + 8 * rows);
-  return hip_status(launch_argmax((const uint16_t*)logits, (int)rows, (int)vocab, ids, ids_bytes, top, keys, ticket,
-                                  reinterpret_cast<hipStream_t>(stream)));
+  if (workspace == nullptr || workspace_bytes < ftk_argmax_workspace_bytes(rows, vocab)) return FTK_ERR_WORKSPACE;
+  return hip_status(launch_argmax((const uint16_t*)logits, (int)rows, (int)vocab, ids, ids_bytes, top,
+                                  (unsigned long long*)workspace, reinterpret_cast<hipStream_t>(stream)));
 }
 
 int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream) {

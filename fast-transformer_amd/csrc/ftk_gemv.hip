@@ -18,9 +18,9 @@
 //   * Each row's 64 lane partials are summed with a DPP tree; the result is
 //     rounded to BF16 once.
 //   * Argmax: per-row keys (orderable BF16 value, inverted index) reduced by
-//     max within the wave, the workgroup, then one 64-bit atomicMax per
-//     workgroup and input row; the last workgroup (ticket counter) writes the
-//     ids and clears the workspace. max is order-independent, so the result
+//     max within the wave and the workgroup, stored per workgroup; a second
+//     small kernel reduces the workgroups (the two stages of
+//     engine/kernels/argmax.py:19-48). max is order-independent, so the result
 //     is deterministic and equals torch.argmax's lowest-index rule.
 #include "ftk_device.h"
 #include "ftk_internal.h"
@@ -32,13 +32,43 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
   extern __shared__ u32x4_t xs[];  // x as [MR][K/8] chunks of 8 BF16
   __shared__ float red[kWaves][MR];
   __shared__ unsigned long long best_lds[kWaves][MR];
-  __shared__ int is_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int K = a.K;
   const int KC = K >> 3;           // 16-byte chunks per row
+
+  // ---- the weight rows this wave streams -------------------------------------
+  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per wave per tile
+  const int outputs = gemv_outputs(EPI, a.N);
+  unsigned long long best[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) best[m] = 0ull;
+
+  // This lane's first chunk of every weight row the wave reads for ``tile``.
+  auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int col = gemv_output(tile, wave, p, PW);
+      const int c = col < outputs ? col : outputs - 1;  // clamp: loads stay in bounds
+      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + lane * 8;
+      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + lane * 8;
+    }
+  };
+
+  const uint16_t* wr[RPW];
+  const bool full = KC % (64 * U) == 0;
+  u32x4_t pre[U][RPW];
+  if (full) {
+    // The first batch of weight loads goes out before x is staged, so its HBM
+    // latency overlaps the staging instead of following it (grid <= tiles).
+    row_ptrs(blockIdx.x, wr);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) pre[u][r] = load_stream16(wr[r] + (size_t)u * 512);
+  }
 
   // ---- stage x into LDS (and the RMSNorm prologue) ----------------------
   float ss[MR];
@@ -90,24 +120,6 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
   }
   __syncthreads();
 
-  // ---- stream the weight rows ----------------------------------------------
-  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per wave per tile
-  const int outputs = gemv_outputs(EPI, a.N);
-  unsigned long long best[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) best[m] = 0ull;
-
-  // This lane's first chunk of every weight row the wave reads for ``tile``.
-  auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
-#pragma unroll
-    for (int p = 0; p < PW; ++p) {
-      const int col = gemv_output(tile, wave, p, PW);
-      const int c = col < outputs ? col : outputs - 1;  // clamp: loads stay in bounds
-      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + lane * 8;
-      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + lane * 8;
-    }
-  };
-
   // Reduce the lane partials of ``tile``, run the epilogue, clear the accumulators.
   auto finish = [&](int tile, float (&acc)[RPW][MR]) {
     float tot[RPW][MR];
@@ -143,20 +155,28 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
 
-  const uint16_t* wr[RPW];
-  if (KC % (64 * U) == 0) {
+  if (full) {
     // Every lane's chunks are in range: batches of U x RPW 16-byte loads, all
     // issued before the first is consumed. Memory parallelism comes from the
     // batch size and from the other waves resident on the SIMD.
     const int NB = KC / (64 * U);
+    bool first = true;
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-      row_ptrs(tile, wr);
+      if (!first) row_ptrs(tile, wr);
       for (int b = 0; b < NB; ++b) {
         u32x4_t wv[U][RPW];
+        if (first) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+          for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream16(wr[r] + (size_t)(b * U + u) * 512);
+            for (int r = 0; r < RPW; ++r) wv[u][r] = pre[u][r];
+          first = false;
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream16(wr[r] + (size_t)(b * U + u) * 512);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int c = (b * U + u) * 64 + lane;
@@ -194,6 +214,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
+    // This workgroup's best key per input row; the finalize pass reduces the workgroups.
     if (lane == 0) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) best_lds[wave][m] = best[m];
@@ -202,25 +223,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
     if (tid < MR) {
       unsigned long long k = best_lds[0][tid];
       for (int w = 1; w < kWaves; ++w) k = key_max(k, best_lds[w][tid]);
-      atomicMax(a.keys + tid, k);
-      __threadfence();
-    }
-    __syncthreads();
-    if (tid == 0) is_last = (atomicAdd(a.ticket, 1u) == gridDim.x - 1);
-    __syncthreads();
-    if (is_last) {
-      __threadfence();
-      if (tid < MR) {
-        const unsigned long long k = atomicMax(a.keys + tid, 0ull);
-        const uint32_t idx = key_index(k);
-        if (a.ids_bytes == 8)
-          reinterpret_cast<int64_t*>(a.ids)[tid] = (int64_t)idx;
-        else
-          reinterpret_cast<int32_t*>(a.ids)[tid] = (int32_t)idx;
-        if (a.top != nullptr) a.top[tid] = from_orderable((uint32_t)(k >> 32));
-        atomicExch(a.keys + tid, 0ull);
-      }
-      if (tid == 0) atomicExch(a.ticket, 0u);
+      a.keys[(size_t)blockIdx.x * MR + tid] = k;
     }
   }
 }

@@ -20,8 +20,7 @@ struct ProjArgs {
   void* ids;              // [M] int32 or int64
   int ids_bytes;
   float* top;             // [M] winning logit as FP32, or null
-  unsigned long long* keys;  // [M] zeroed workspace (left zeroed on exit)
-  unsigned int* ticket;      // zeroed workspace counter (left zeroed on exit)
+  unsigned long long* keys;  // [grid][M] per-workgroup best keys (workspace)
 };
 
 // Launch shape of the GEMV kind.
@@ -44,6 +43,23 @@ DeviceInfo device_info();
 bool gemv_supported(int M, int rpw, int unroll, int epi);
 hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& shape, hipStream_t stream);
 
+// Launch shape of the MFMA kind.
+struct MfmaShape {
+  int subtiles;  // T: 16-row MFMA subtiles per workgroup
+  int unroll;    // MFMA K steps of weight loads in flight per wave
+  int waves;     // W: waves per workgroup, splitting K
+  int grid;      // workgroups (one per 16 T rows)
+};
+struct MfmaArgs {
+  const float* row_scale;     // [M] RMSNorm scales, written by the prologue pass
+};
+bool mfma_supported(int M, int t, int unroll, int waves, int epi);
+hipError_t launch_mfma(const ProjArgs& a, int epi, const MfmaShape& shape, const MfmaArgs& p, hipStream_t stream);
+
+// Greedy-argmax second stage: ids[m] (and top[m]) from keys[slot * M + m], slot < slots.
+hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
+                                  float* top, hipStream_t stream);
+
 // Ragged or unaligned shapes: one wave per weight row, scalar loads, no prologue/epilogue.
 hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
                                hipStream_t stream);
@@ -57,7 +73,8 @@ hipError_t launch_add_rms_norm(const void* x, int splits, int64_t split_stride, 
 hipError_t launch_swiglu(const void* packed, int splits, int64_t split_stride, uint16_t* out, int rows, int width,
                          hipStream_t stream);
 hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids, int ids_bytes, float* top,
-                         unsigned long long* keys, unsigned int* ticket, hipStream_t stream);
+                         unsigned long long* keys, hipStream_t stream);
+int argmax_blocks(int vocab);
 hipError_t launch_merge_splits(const float* partial, int splits, int64_t count, uint16_t* out, hipStream_t stream);
 
 }  // namespace ftk

@@ -2,7 +2,7 @@
 //   rms_norm       engine/kernels/rmsnorm.py:21-72
 //   add_rms_norm   engine/kernels/rmsnorm.py:75-125 (BF16 input or FP32 split partials)
 //   swiglu         engine/kernels/swiglu.py:13-40   (BF16 input or FP32 split partials)
-//   argmax         engine/kernels/argmax.py:19-70   (lowest index on ties)
+//   argmax         engine/kernels/argmax.py:19-70   (lowest index on ties; two stages)
 //   merge_splits   engine/kernels/linear.py:81-93, engine/kernels/merged.py:37-45
 // These are small, launch-bound kernels; the projections fold the norm, SwiGLU
 // and argmax into themselves and do not need them.
@@ -84,15 +84,25 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const void* __restrict
   out[i] = (uint16_t)swiglu_bf16(g, u);
 }
 
-// One workgroup per (row, column block of 8192): block key max, one atomicMax
-// per workgroup and row, the last workgroup writes ids and clears the workspace.
+// Stage one: one workgroup per (row, column block of 8192) reduces its block to
+// a key (orderable BF16 value, inverted index) and stores it (argmax.py:19-31).
 constexpr int kArgmaxBlock = 8192;
 
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int vocab, void* ids,
-                                                          int ids_bytes, float* top, unsigned long long* keys,
-                                                          unsigned int* ticket, int rows) {
+int argmax_blocks(int vocab) { return (vocab + kArgmaxBlock - 1) / kArgmaxBlock; }
+
+__device__ __forceinline__ unsigned long long block_max_key(unsigned long long v, unsigned long long* red) {
+  red[threadIdx.x] = v;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = key_max(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  return red[0];
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_block_kernel(const uint16_t* __restrict__ logits, int vocab,
+                                                                unsigned long long* __restrict__ keys, int rows) {
   __shared__ unsigned long long red[kThreads];
-  __shared__ int is_last;
   const int row = blockIdx.y;
   const int begin = blockIdx.x * kArgmaxBlock;
   const int end = min(begin + kArgmaxBlock, vocab);
@@ -100,31 +110,27 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const uint16_t* __rest
   unsigned long long best = 0ull;
   for (int c = begin + threadIdx.x; c < end; c += kThreads)
     best = key_max(best, argmax_key(bf16_to_f32(lr[c]), (uint32_t)c));
-  red[threadIdx.x] = best;
-  __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = key_max(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
-  }
+  best = block_max_key(best, red);
+  if (threadIdx.x == 0) keys[(size_t)blockIdx.x * rows + row] = best;  // [slot][row]
+}
+
+// Stage two: one workgroup per row picks the best of ``slots`` keys and writes
+// the id (and the winning logit) (argmax.py:34-48 _first_best).
+__global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
+                                                                   int slots, int rows, void* ids, int ids_bytes,
+                                                                   float* top) {
+  __shared__ unsigned long long red[kThreads];
+  const int row = blockIdx.x;
+  unsigned long long best = 0ull;
+  for (int s = threadIdx.x; s < slots; s += kThreads) best = key_max(best, keys[(size_t)s * rows + row]);
+  best = block_max_key(best, red);
   if (threadIdx.x == 0) {
-    atomicMax(keys + row, red[0]);
-    __threadfence();
-    is_last = (atomicAdd(ticket, 1u) == gridDim.x * gridDim.y - 1);
-  }
-  __syncthreads();
-  if (is_last) {
-    __threadfence();
-    for (int r = threadIdx.x; r < rows; r += kThreads) {
-      const unsigned long long k = atomicMax(keys + r, 0ull);
-      const uint32_t idx = key_index(k);
-      if (ids_bytes == 8)
-        reinterpret_cast<int64_t*>(ids)[r] = (int64_t)idx;
-      else
-        reinterpret_cast<int32_t*>(ids)[r] = (int32_t)idx;
-      if (top != nullptr) top[r] = from_orderable((uint32_t)(k >> 32));
-      atomicExch(keys + r, 0ull);
-    }
-    if (threadIdx.x == 0) atomicExch(ticket, 0u);
+    const uint32_t idx = key_index(best);
+    if (ids_bytes == 8)
+      reinterpret_cast<int64_t*>(ids)[row] = (int64_t)idx;
+    else
+      reinterpret_cast<int32_t*>(ids)[row] = (int32_t)idx;
+    if (top != nullptr) top[row] = from_orderable((uint32_t)(best >> 32));
   }
 }
 
@@ -161,10 +167,18 @@ hipError_t launch_swiglu(const void* packed, int splits, int64_t split_stride, u
 }
 
 hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids, int ids_bytes, float* top,
-                         unsigned long long* keys, unsigned int* ticket, hipStream_t stream) {
-  const int blocks = (vocab + kArgmaxBlock - 1) / kArgmaxBlock;
-  hipLaunchKernelGGL(argmax_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, ids, ids_bytes,
-                     top, keys, ticket, rows);
+                         unsigned long long* keys, hipStream_t stream) {
+  const int blocks = argmax_blocks(vocab);
+  hipLaunchKernelGGL(argmax_block_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, keys, rows);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_argmax_finalize(keys, blocks, rows, ids, ids_bytes, top, stream);
+}
+
+hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
+                                  float* top, hipStream_t stream) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(kThreads), 0, stream, keys, slots, M, ids, ids_bytes,
+                     top);
   return hipGetLastError();
 }
 

@@ -49,10 +49,37 @@ FTK_HD int gemv_weight_row(int epi, int col, int half, int n_rows) {
   return epi == EPI_SWIGLU ? col + half * (n_rows / 2) : col;
 }
 
-// ---- M >= 4: BF16 MFMA skinny GEMM (16 weight rows per wave subtile) ------
+// ---- M >= 4: BF16 MFMA skinny GEMM (T subtiles of 16 weight rows per workgroup)
 
-constexpr int kMfmaRows = 16;       // weight rows per MFMA subtile (v_mfma_f32_16x16x32_bf16)
-constexpr int kMfmaK = 32;          // K per MFMA step
+constexpr int kMfmaK = 32;          // K per MFMA step (v_mfma_f32_16x16x32_bf16)
+
+// Outputs one workgroup produces: 16 T rows, or 8 T gate/up pairs.
+FTK_HD int mfma_out_per_tile(int epi, int t) { return epi == EPI_SWIGLU ? 8 * t : 16 * t; }
+
+FTK_HD int mfma_tiles(int epi, int n_rows, int t) {
+  const int per = mfma_out_per_tile(epi, t);
+  return (gemv_outputs(epi, n_rows) + per - 1) / per;
+}
+
+// Weight row that lane ``li`` (0..15) of subtile ``sub`` reads in ``tile``, clamped in bounds.
+// SwiGLU: subtiles [0, T/2) are gate rows, [T/2, T) the matching up rows (cat(W_gate, W_up)).
+FTK_HD int mfma_weight_row(int epi, int tile, int sub, int li, int n_rows, int t) {
+  if (epi == EPI_SWIGLU) {
+    const int half = n_rows / 2;
+    const int up = sub >= t / 2 ? 1 : 0;
+    const int col = tile * 8 * t + (sub - up * (t / 2)) * 16 + li;
+    return (col < half ? col : half - 1) + up * half;
+  }
+  const int r = tile * 16 * t + sub * 16 + li;
+  return r < n_rows ? r : n_rows - 1;
+}
+
+// ---- workspace layout of one projection call (bytes) -----------------------
+// Nothing in it carries state between calls: every slot a kernel reads was
+// written earlier in the same call (row scales by the prologue pass, argmax
+// keys by every workgroup), so no zeroing or clearing protocol is needed.
+constexpr int64_t kWsScale = 0;     // [32] f32 RMSNorm row scales (MFMA kind)
+constexpr int64_t kWsKeys = 256;    // [grid][M] u64 per-workgroup greedy-argmax keys
 
 // Persistent launch: the fewest programs that keep the deepest walk at
 // ceil(tiles / units) (the rule of engine/kernels/gemm.py:330-338).

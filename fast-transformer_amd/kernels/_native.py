@@ -23,12 +23,13 @@ _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, c
 
 
 class Config(ctypes.Structure):
-    """ftk_config: a launch choice (kind, rows_per_wave, unroll, groups_per_cu); zeros = planner default."""
+    """ftk_config: a launch choice (kind, rows_per_wave, unroll, groups_per_cu, waves); zeros = planner default."""
 
-    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("groups_per_cu", _int)]
+    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("groups_per_cu", _int),
+                ("waves", _int)]
 
     def key(self):
-        return (self.kind, self.rows_per_wave, self.unroll, self.groups_per_cu)
+        return (self.kind, self.rows_per_wave, self.unroll, self.groups_per_cu, self.waves)
 
     def __repr__(self):
         return f"Config{self.key()}"
@@ -36,7 +37,8 @@ class Config(ctypes.Structure):
 
 class Plan(ctypes.Structure):
     _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("grid", _int), ("tiles", _int),
-                ("threads", _int), ("lds_bytes", _i64)]
+                ("threads", _int), ("lds_bytes", _i64), ("splits", _int), ("k_slice", _int),
+                ("workspace_bytes", _i64)]
 
 
 # name -> (restype, argtypes), exactly the declarations of include/ftk.h
@@ -60,7 +62,8 @@ SIGNATURES = {
     "ftk_swiglu_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _i64, _i64, _c_void_p]),
     "ftk_argmax_bf16": (_int, [_c_void_p, _i64, _i64, _c_void_p, _int, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "ftk_merge_splits_bf16": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
-    "ftk_argmax_workspace_bytes": (_i64, [_i64]),
+    "ftk_argmax_workspace_bytes": (_i64, [_i64, _i64]),
+    "ftk_project_workspace_bytes": (_i64, [_i64, _i64, _i64, _int, ctypes.POINTER(Config)]),
     "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
     "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
                                  ctypes.POINTER(_i64)]),
@@ -128,15 +131,36 @@ def require_gpu(*tensors):
 
 
 _WORKSPACES = {}
+#: Every workspace ever handed to a kernel stays alive: a captured graph keeps its address.
+_RETIRED = []
 
 
-def argmax_workspace(device, rows):
-    """Per-device zeroed argmax workspace (the kernels leave it zeroed after each call)."""
-    need = int(lib().ftk_argmax_workspace_bytes(rows))
-    ws = _WORKSPACES.get(device)
+def workspace(device, need, purpose):
+    """Per-device, per-purpose scratch buffer of at least ``need`` bytes.
+
+    The kernels keep only per-call scratch there (per-workgroup argmax keys,
+    RMSNorm row scales), written before it is read in the same call, so no
+    initial contents are needed. A buffer only grows, outside graph capture;
+    a replaced buffer is kept alive for graphs that captured its address.
+    """
+    key = (device, purpose)
+    ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
         if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("argmax workspace must be allocated during eager warmup, before graph capture")
-        ws = torch.zeros(max(need, 4096), dtype=torch.uint8, device=device)
-        _WORKSPACES[device] = ws
+            raise RuntimeError("the kernels' workspace must be sized during eager warmup, before graph capture")
+        size = max(int(need), 1 << 20, 2 * (ws.numel() if ws is not None else 0))
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
     return ws
+
+
+def argmax_workspace(device, rows, vocab):
+    """Workspace of the standalone argmax for ``rows`` rows of ``vocab`` logits."""
+    return workspace(device, int(lib().ftk_argmax_workspace_bytes(rows, vocab)), "argmax")
+
+
+def project_workspace(device, m, n, k, epilogue, config=None):
+    """Workspace of one projection call (split-K partials, row scales, argmax keys)."""
+    return workspace(device, int(lib().ftk_project_workspace_bytes(m, n, k, epilogue, config)), "project")

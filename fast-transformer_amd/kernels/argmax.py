@@ -6,10 +6,11 @@ signatures and int64 results. Ties resolve to the lowest index and NaN counts
 as the maximum, torch.argmax's rule; BF16 -> FP32 is exact, so the answer is
 identical to torch.argmax of the BF16 logits.
 
-Device scheme: each workgroup reduces its logits to a 64-bit key (orderable
-BF16 value << 32 | ~index) and folds it into a per-row slot with one atomicMax;
-the last workgroup to finish (ticket counter) writes the ids and clears the
-workspace. max is order-independent, so results are deterministic.
+Device scheme (the reference's two stages, argmax.py:19-48): each workgroup
+reduces its logits to a 64-bit key per row (orderable BF16 value << 32 |
+~index) and stores it; a second small kernel takes the max over the
+workgroups and writes the ids. max is order-independent, so results are
+deterministic, and no workgroup ever waits on another.
 
 ``lm_head_argmax`` is the fused final-norm + lm_head + argmax kernel: the
 vocabulary GEMV rounds each logit to BF16 and reduces it in its epilogue,
@@ -30,7 +31,7 @@ def argmax(logits, block=8192, top=None):
     vocab = logits.shape[-1]
     rows = logits.numel() // vocab
     out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=logits.device)
-    ws = _native.argmax_workspace(logits.device, rows)
+    ws = _native.argmax_workspace(logits.device, rows, vocab)
     if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < rows):
         raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
     _native.call("ftk_argmax_bf16", _native.ptr(logits), rows, vocab, _native.ptr(out), 8, _native.ptr(top),
@@ -52,7 +53,7 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     v = weight.shape[0]
     ids = torch.empty(shape[:-1], dtype=ids_dtype, device=x.device)
     out = torch.empty((*shape[:-1], v), dtype=torch.bfloat16, device=x.device) if logits else None
-    ws = _native.argmax_workspace(x.device, m)
+    ws = _native.project_workspace(x.device, m, v, k, _native.EPI_ARGMAX, config)
     ids_bytes = {torch.int64: 8, torch.int32: 4}[ids_dtype]
     status = _native.try_call(
         "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),

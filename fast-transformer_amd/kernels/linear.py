@@ -60,12 +60,16 @@ def project(x, weight, config=None, out=None):
         raise ValueError(f"x has K={k}, weight has K={weight.shape[1]}")
     if out is None:
         out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
-    stream = _native.stream_of(x)
-    if config is None:
-        _native.call("ftk_linear_bf16", _native.ptr(x), _native.ptr(weight), _native.ptr(out), m, n, k, stream)
-    else:
-        _native.call("ftk_project_bf16", _native.ptr(x), None, 0.0, _native.ptr(weight), _native.ptr(out), m, n, k,
-                     _native.EPI_STORE, None, 0, None, None, 0, config, stream)
+    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config)
+    status = _native.try_call("ftk_project_bf16", _native.ptr(x), None, 0.0, _native.ptr(weight), _native.ptr(out),
+                              m, n, k, _native.EPI_STORE, None, 0, None, _native.ptr(ws), ws.numel(), config,
+                              _native.stream_of(x))
+    if status == _native.FTK_ERR_UNSUPPORTED and config is None:
+        # unaligned pointers: the generic kind takes any alignment
+        _native.call("ftk_linear_bf16", _native.ptr(x), _native.ptr(weight), _native.ptr(out), m, n, k,
+                     _native.stream_of(x))
+    elif status != _native.FTK_OK:
+        raise _native.FtkError("ftk_project_bf16", status)
     return out
 
 
@@ -82,9 +86,11 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
     m, k = flat.shape
     n = weight.shape[0]
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config)
     status = _native.try_call(
         "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
-        _native.ptr(out), m, n, k, _native.EPI_STORE, None, 0, None, None, 0, config, _native.stream_of(flat))
+        _native.ptr(out), m, n, k, _native.EPI_STORE, None, 0, None, _native.ptr(ws), ws.numel(), config,
+        _native.stream_of(flat))
     if status == _native.FTK_ERR_UNSUPPORTED:
         from kernels.rmsnorm import rms_norm
         return linear(rms_norm(x, norm_weight, eps), weight)
@@ -95,12 +101,16 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
 
 def _candidates(m, n, k):
     """Launch shapes worth timing for one (M, N, K): planner default first."""
-    if m > 4 or k % 8:
+    if k % 8:
         return [None]
     configs = [None]
-    for rpw, unroll in ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)):
-        for gpc in (4, 8):
-            configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc))
+    if m <= 4:
+        for rpw, unroll in ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)):
+            for gpc in (4, 8):
+                configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc))
+    for rows, unroll, waves in ((16, 4, 4), (16, 8, 4), (16, 4, 8), (16, 8, 8), (16, 4, 16), (32, 4, 4),
+                                (32, 8, 4), (32, 4, 8), (32, 8, 8), (32, 4, 16), (64, 2, 4), (64, 4, 4), (64, 2, 8)):
+        configs.append(_native.Config(_native.KIND_MFMA, rows, unroll, 0, waves))
     return configs
 
 

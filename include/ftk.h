@@ -19,9 +19,11 @@
  *     code other than FTK_OK or FTK_ERR_HIP is returned.
  *   - M (rows of x) is 1..FTK_MAX_ROWS, as the reference's MAX_ROWS = 32
  *     (engine/kernels/linear.py:343); larger M is the caller's native GEMM.
- *   - Workspaces (argmax) must be zero-filled once when allocated; every
- *     completed call leaves them zeroed. Calls that share a workspace must not
- *     run concurrently.
+ *   - Workspaces hold per-call scratch only (per-workgroup argmax keys,
+ *     RMSNorm row scales): no initial contents are required and nothing carries
+ *     over between calls. Calls that share a workspace must not run
+ *     concurrently. No kernel waits on another workgroup: there are no
+ *     device-scope fences or tickets anywhere.
  */
 #ifndef FTK_H
 #define FTK_H
@@ -60,19 +62,24 @@ typedef enum ftk_kind {
  * Zero fields mean "planner default". */
 typedef struct ftk_config {
   int kind;            /* ftk_kind */
-  int rows_per_wave;   /* GEMV: weight rows per wave per tile (2, 4, 8) */
-  int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4) */
-  int groups_per_cu;   /* grid cap = groups_per_cu * compute units (grid-stride beyond) */
+  int rows_per_wave;   /* GEMV: weight rows per wave per tile (2, 4, 8); MFMA: rows per workgroup (16, 32, 64) */
+  int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
+                          MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4) */
+  int groups_per_cu;   /* GEMV: grid cap = groups_per_cu * CUs (grid-stride beyond); MFMA: unused */
+  int waves;           /* MFMA: waves per workgroup splitting K (4, 8, 16); GEMV: unused (4) */
 } ftk_config;
 
 typedef struct ftk_plan {
   int kind;
   int rows_per_wave;
   int unroll;
-  int grid;            /* workgroups launched */
-  int tiles;           /* row tiles walked grid-stride */
-  int threads;         /* threads per workgroup */
-  int64_t lds_bytes;   /* dynamic LDS per workgroup */
+  int grid;                 /* workgroups launched */
+  int tiles;                /* row tiles (GEMV: walked grid-stride; MFMA: 64 rows each) */
+  int threads;              /* threads per workgroup (64 per wave) */
+  int64_t lds_bytes;        /* dynamic LDS per workgroup */
+  int splits;               /* K slices per output (always 1: no split-K across workgroups) */
+  int k_slice;              /* K elements per slice (= K) */
+  int64_t workspace_bytes;  /* workspace this launch needs (0 = none) */
 } ftk_plan;
 
 /* ---- library ------------------------------------------------------------- */
@@ -111,6 +118,11 @@ int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const v
                             int ids_bytes, float* top, int64_t M, int64_t V, int64_t K, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes ftk_project_bf16 needs for this shape on the current device:
+ * per-workgroup argmax keys (FTK_EPI_ARGMAX) and the RMSNorm row scales of the
+ * MFMA kind (gamma != NULL, M > 4). Other calls need none (NULL is fine). */
+int64_t ftk_project_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue, const ftk_config* cfg);
+
 /* General form of the three above with an explicit launch choice (cfg may be
  * NULL): the tuner's entry point (engine/kernels/linear.py:436-481 _choose). */
 int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M, int64_t N,
@@ -143,8 +155,8 @@ int ftk_argmax_bf16(const void* logits, int64_t rows, int64_t vocab, void* ids, 
 /* bf16(sum of FP32 split partials) (engine/kernels/linear.py:81-93 _merge_projection). */
 int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream);
 
-/* Workspace bytes of the argmax entry points for `rows` rows. */
-int64_t ftk_argmax_workspace_bytes(int64_t rows);
+/* Workspace bytes of ftk_argmax_bf16 for `rows` rows of `vocab` logits. */
+int64_t ftk_argmax_workspace_bytes(int64_t rows, int64_t vocab);
 
 /* ---- planning (host only, no device needed) ---------------------------------- */
 

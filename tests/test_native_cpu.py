@@ -43,8 +43,8 @@ def test_version_and_status_strings():
     assert b"gfx950" in lib.ftk_version()
     for code in range(5):
         assert lib.ftk_status_string(code)
-    assert lib.ftk_argmax_workspace_bytes(1) == 16
-    assert lib.ftk_argmax_workspace_bytes(32) == 8 * 32 + 8
+    assert lib.ftk_argmax_workspace_bytes(1, 8192) == 8
+    assert lib.ftk_argmax_workspace_bytes(32, 151936) == 8 * 32 * 19
 
 
 def test_invalid_arguments_rejected_before_any_launch():
@@ -57,6 +57,9 @@ def test_invalid_arguments_rejected_before_any_launch():
     fake = ctypes.c_void_p(16)
     # argmax without a workspace
     assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 8, None, None, 0, None) == _native.FTK_ERR_WORKSPACE
+    # a fused argmax projection without its key workspace
+    assert lib.ftk_project_bf16(fake, None, 0.0, fake, None, 1, 64, 64, _native.EPI_ARGMAX, fake, 8, None, None, 0,
+                                None, None) in (_native.FTK_ERR_WORKSPACE, _native.FTK_ERR_HIP)
     assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 3, None, fake, 64, None) == _native.FTK_ERR_INVALID
 
 
@@ -82,15 +85,28 @@ def _coverage(plan, n, epilogue):
     return np.frombuffer(counts, dtype=np.int32), max_row.value
 
 
+def _configs(m):
+    if m <= 4:
+        gemv = [_native.Config(_native.KIND_GEMV, rpw, u, gpc) for rpw, u in ((2, 4), (4, 2), (8, 1)) for gpc in (1, 8)]
+    else:
+        gemv = []
+    mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
+            for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
+    return [None] + gemv + mfma
+
+
 @pytest.mark.parametrize("n,k", SHAPES)
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16, 17, 32])
 def test_plan_writes_every_output_once(m, n, k):
     for epilogue in (_native.EPI_STORE, _native.EPI_SWIGLU, _native.EPI_ARGMAX):
         if epilogue == _native.EPI_SWIGLU and n % 2:
             continue
-        for cfg in [None] + [_native.Config(0, rpw, u, gpc) for rpw, u in ((2, 4), (4, 2), (8, 1)) for gpc in (1, 8)]:
+        for cfg in _configs(m):
             if cfg is not None and k % 8:
                 continue
+            if (cfg is not None and cfg.kind == _native.KIND_MFMA and cfg.rows_per_wave == 16
+                    and epilogue == _native.EPI_SWIGLU):
+                continue  # a SwiGLU workgroup needs a gate and an up subtile
             p = _native.Plan()
             status = _native.lib().ftk_plan_project(m, n, k, epilogue, 256, cfg, p)
             if k % 8 and epilogue != _native.EPI_STORE:
@@ -100,9 +116,14 @@ def test_plan_writes_every_output_once(m, n, k):
             counts, max_row = _coverage(p, n, epilogue)
             assert np.all(counts == 1), (m, n, k, epilogue, cfg)
             assert max_row == n - 1
-            assert p.grid >= 1 and p.grid <= max(p.tiles, 1)
             if p.kind == _native.KIND_GEMV:
+                assert 1 <= p.grid <= p.tiles
                 assert p.lds_bytes == m * k * 2
+            if p.kind == _native.KIND_MFMA:
+                # one workgroup per tile over all of K: no split-K, nothing shared between workgroups
+                assert p.grid == p.tiles and p.splits == 1 and p.k_slice == k
+            if epilogue == _native.EPI_ARGMAX and p.kind != _native.KIND_GENERIC:
+                assert p.workspace_bytes >= 256 + 8 * m * p.grid  # one key per workgroup and row
 
 
 def test_plan_kinds():
@@ -111,3 +132,7 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_GEMV and p.threads == 256
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
+    assert p.kind == _native.KIND_MFMA and p.grid == 256 and p.splits == 1
+    _native.call("ftk_plan_project", 16, 24576, 4096, _native.EPI_SWIGLU, 256, None, p)
+    assert p.kind == _native.KIND_MFMA and p.rows_per_wave == 32 and p.grid == 12288 // 16
