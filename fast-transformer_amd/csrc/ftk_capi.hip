@@ -36,9 +36,35 @@ DeviceInfo device_info() {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Planner defaults (from the launch-shape sweeps on MI355X).
-constexpr int kDefaultRpw = 2;
-constexpr int kDefaultUnroll = 4;
-constexpr int kDefaultGroupsPerCu = 8;
+constexpr int kDefaultGroupsPerCu = 16;
+
+// GEMV launch shape by problem size, measured at M = 1 on the Qwen3 shapes:
+// few outputs want K split across the waves (more workgroups in flight),
+// long rows want more 16-byte loads in flight per wave.
+struct GemvDefault {
+  int rpw, unroll, kw;
+};
+static GemvDefault gemv_default(int epi, int64_t N, int64_t K) {
+  const int64_t outputs = gemv_outputs(epi, (int)N);
+  const int64_t kc = K / 8;
+  GemvDefault d;
+  if (outputs <= 1024)
+    d = {1, 1, 4};          // 0.6B O / down
+  else if (outputs <= 4096 && K >= 8192)
+    d = {2, 4, 2};          // 8B down
+  else if (outputs <= 4096)
+    d = {1, 2, 2};          // 8B O, 0.6B QKV
+  else if (outputs >= 12288)
+    d = {2, 2, 4};          // gate/up, lm_head
+  else
+    d = {2, 4, 1};          // 8B QKV
+  // Keep the unrolled batches whole (the pipelined path needs K % (512 U KW) == 0).
+  while (d.unroll > 1 && kc % (64 * d.unroll * d.kw)) d.unroll /= 2;
+  while (d.kw > 1 && kc % (64 * d.unroll * d.kw)) d.kw /= 2;
+  if (epi == FTK_EPI_SWIGLU && d.rpw % 2) d.rpw = 2;
+  if (!gemv_supported(1, d.rpw, d.unroll, d.kw, epi)) d = {2, 4, 1};  // always instantiated
+  return d;
+}
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
 
@@ -62,24 +88,28 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->grid = p->tiles;
     p->rows_per_wave = 1;
     p->unroll = 1;
+    p->waves = 1;
     return FTK_OK;
   }
   if (K % 8 != 0) return FTK_ERR_UNSUPPORTED;
   if (kind == FTK_KIND_GEMV) {
     if (M > 4) return FTK_ERR_UNSUPPORTED;
-    const int rpw = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : kDefaultRpw;
-    const int unroll = cfg && cfg->unroll ? cfg->unroll : kDefaultUnroll;
+    const GemvDefault d = gemv_default(epi, N, K);
+    const bool given = cfg && cfg->rows_per_wave;
+    const int rpw = given ? cfg->rows_per_wave : d.rpw;
+    const int unroll = cfg && cfg->unroll ? cfg->unroll : (given ? 2 : d.unroll);
     const int gpc = cfg && cfg->groups_per_cu ? cfg->groups_per_cu : kDefaultGroupsPerCu;
-    if (!gemv_supported((int)M, rpw, unroll, epi)) return FTK_ERR_INVALID;
-    if (epi == FTK_EPI_SWIGLU && rpw % 2) return FTK_ERR_INVALID;
+    const int kw = cfg && cfg->waves ? cfg->waves : (given ? 1 : d.kw);
+    if (!gemv_supported((int)M, rpw, unroll, kw, epi)) return FTK_ERR_INVALID;
     p->rows_per_wave = rpw;
     p->unroll = unroll;
-    p->tiles = gemv_tiles(epi, (int)N, rpw);
+    p->waves = kw;
+    p->tiles = gemv_tiles(epi, (int)N, rpw, kw);
     const int64_t cap = (int64_t)gpc * cus;
     p->grid = (int)(p->tiles < cap ? p->tiles : cap);
-    p->lds_bytes = M * K * 2;
+    p->lds_bytes = M * K * 2;  // + K * 2 for the staged gain when the prologue is on
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
-    if (p->lds_bytes > 160 * 1024) return FTK_ERR_UNSUPPORTED;
+    if (p->lds_bytes + K * 2 > 160 * 1024) return FTK_ERR_UNSUPPORTED;
     return FTK_OK;
   }
   if (kind == FTK_KIND_MFMA) {
@@ -93,6 +123,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     if (!mfma_supported((int)M, t, unroll, waves, epi)) return FTK_ERR_INVALID;
     p->rows_per_wave = rows;
     p->unroll = unroll;
+    p->waves = waves;
     p->threads = 64 * waves;
     p->tiles = mfma_tiles(epi, (int)N, t);
     p->grid = p->tiles;
@@ -190,12 +221,13 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
   }
   if (p->kind != FTK_KIND_GEMV) return FTK_ERR_UNSUPPORTED;
   const int pw = gemv_per_wave(epilogue, p->rows_per_wave);
+  const int groups = gemv_groups(p->waves);
   const int halves = epilogue == FTK_EPI_SWIGLU ? 2 : 1;
   for (int b = 0; b < p->grid; ++b)
     for (int tile = b; tile < p->tiles; tile += p->grid)
-      for (int w = 0; w < kWaves; ++w)
+      for (int w = 0; w < groups; ++w)
         for (int s = 0; s < pw; ++s) {
-          const int col = gemv_output(tile, w, s, pw);
+          const int col = gemv_output(tile, w, s, pw, groups);
           const int clamped = col < outputs ? col : (int)outputs - 1;
           for (int h = 0; h < halves; ++h) {
             const int64_t row = gemv_weight_row(epilogue, clamped, h, (int)N);
@@ -246,10 +278,10 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   hipError_t e;
   if (p.kind == FTK_KIND_GEMV) {
-    GemvShape g = {p.rows_per_wave, p.unroll, p.grid, p.tiles, (size_t)p.lds_bytes};
+    GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);
   } else {
-    MfmaShape shape = {p.rows_per_wave / 16, p.unroll, p.threads / 64, p.grid};
+    MfmaShape shape = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid};
     MfmaArgs m;
     m.row_scale = gamma != nullptr ? (const float*)(ws + kWsScale) : nullptr;
     e = launch_mfma(a, epilogue, shape, m, s);

@@ -10,55 +10,63 @@
 // Layout and schedule:
 //   * A workgroup is 4 waves. It stages x (normalised when the prologue is on)
 //     in LDS once, then walks row tiles grid-stride.
-//   * A wave owns RPW whole weight rows per tile. Lane l reads 16-byte chunks
-//     l, l+64, l+128, ... of each row, so every wave-wide load is 1 KiB of
-//     contiguous HBM; loads are non-temporal (weights are read exactly once).
+//   * The 4 waves form 4 / KW row groups; a group owns RPW whole weight rows
+//     per tile and its KW waves split K by interleaved 1 KiB chunk blocks
+//     (KW > 1 gives small-N shapes enough workgroups). Lane l of a wave reads
+//     16-byte chunks l, l + 64, ... of its blocks, so every wave-wide load is
+//     1 KiB of contiguous HBM; loads are non-temporal (weights are read once).
+//   * The first batch of weight loads is issued before x is staged.
 //   * Products use v_dot2_f32_bf16 (two exact BF16 products + FP32 add per
 //     instruction, no unpacking), accumulating per lane in FP32.
-//   * Each row's 64 lane partials are summed with a DPP tree; the result is
-//     rounded to BF16 once.
+//   * Each row's lane partials are summed with a DPP tree, the KW wave totals
+//     in LDS in wave order; the result is rounded to BF16 once.
 //   * Argmax: per-row keys (orderable BF16 value, inverted index) reduced by
-//     max within the wave and the workgroup, stored per workgroup; a second
-//     small kernel reduces the workgroups (the two stages of
-//     engine/kernels/argmax.py:19-48). max is order-independent, so the result
-//     is deterministic and equals torch.argmax's lowest-index rule.
+//     max within the workgroup and stored per workgroup; a second small kernel
+//     reduces the workgroups (the two stages of engine/kernels/argmax.py:19-48).
+//     max is order-independent, so the result is deterministic and equals
+//     torch.argmax's lowest-index rule. No workgroup ever waits on another.
 #include "ftk_device.h"
 #include "ftk_internal.h"
 
 namespace ftk {
 
-template <int MR, int RPW, int U, bool PRO, int EPI>
+template <int MR, int RPW, int U, int KW, bool PRO, int EPI>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
-  extern __shared__ u32x4_t xs[];  // x as [MR][K/8] chunks of 8 BF16
+  extern __shared__ u32x4_t xs[];  // x as [MR][K/8] chunks of 8 BF16 (+ the gain when PRO)
   __shared__ float red[kWaves][MR];
+  __shared__ float part[kWaves][RPW][MR];
   __shared__ unsigned long long best_lds[kWaves][MR];
 
+  constexpr int GROUPS = kWaves / KW;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int grp = wave / KW, kw = wave - grp * KW;
   const int K = a.K;
-  const int KC = K >> 3;           // 16-byte chunks per row
+  const int KC = K >> 3;  // 16-byte chunks per row
 
   // ---- the weight rows this wave streams -------------------------------------
-  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per wave per tile
+  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per row group per tile
   const int outputs = gemv_outputs(EPI, a.N);
   unsigned long long best[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) best[m] = 0ull;
 
-  // This lane's first chunk of every weight row the wave reads for ``tile``.
+  // This lane's first chunk (block kw) of every weight row the group reads for ``tile``.
   auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
-      const int col = gemv_output(tile, wave, p, PW);
+      const int col = gemv_output(tile, grp, p, PW, GROUPS);
       const int c = col < outputs ? col : outputs - 1;  // clamp: loads stay in bounds
-      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + lane * 8;
-      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + lane * 8;
+      const size_t first = (size_t)(kw * 64 + lane) * 8;
+      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + first;
+      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + first;
     }
   };
 
   const uint16_t* wr[RPW];
-  const bool full = KC % (64 * U) == 0;
+  const bool full = KC % (64 * U * KW) == 0;
+  constexpr size_t kStep = (size_t)KW * 512;  // elements between this wave's consecutive chunk blocks
   u32x4_t pre[U][RPW];
   if (full) {
     // The first batch of weight loads goes out before x is staged, so its HBM
@@ -67,10 +75,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) pre[u][r] = load_stream16(wr[r] + (size_t)u * 512);
+      for (int r = 0; r < RPW; ++r) pre[u][r] = load_stream16(wr[r] + u * kStep);
   }
 
-  // ---- stage x into LDS (and the RMSNorm prologue) ----------------------
+  // ---- stage x (and the RMSNorm gain) into LDS, then the prologue ----------
+  // The gain is staged in the same pass as x, so the prologue pays one load
+  // latency (hidden behind the weight prefetch above), not two in sequence.
+  u32x4_t* gs = xs + MR * KC;  // [K/8] gain chunks, prologue only
+  if constexpr (PRO) {
+    for (int c = tid; c < KC; c += kThreads) gs[c] = load16(a.gamma + (size_t)c * 8);
+  }
   float ss[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
@@ -79,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
       const u32x4_t v = load16(a.x + (size_t)m * K + (size_t)c * 8);
       xs[m * KC + c] = v;
       if constexpr (PRO) {
-        const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
@@ -103,13 +117,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
       const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
       for (int c = tid; c < KC; c += kThreads) {
         const u32x4_t v = xs[m * KC + c];
-        const u32x4_t g = load16(a.gamma + (size_t)c * 8);
-        const uint32_t e[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t ge[4] = {g.x, g.y, g.z, g.w};
+        const u32x4_t g = gs[c];
+        const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+        const uint32_t ge[4] = {g[0], g[1], g[2], g[3]};
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // bf16(x * rsqrt) first, then the gamma multiply, rounded again.
+          // bf16(x * rsqrt) first, then the gain multiply, rounded again.
           const float nlo = round_bf16(lo_f32(e[i]) * scale);
           const float nhi = round_bf16(hi_f32(e[i]) * scale);
           o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
@@ -120,7 +134,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
   }
   __syncthreads();
 
-  // Reduce the lane partials of ``tile``, run the epilogue, clear the accumulators.
+  // Reduce the partials of ``tile`` (lanes, then the group's KW waves in wave
+  // order), run the epilogue on the group's first wave, clear the accumulators.
   auto finish = [&](int tile, float (&acc)[RPW][MR]) {
     float tot[RPW][MR];
 #pragma unroll
@@ -130,9 +145,29 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
         tot[r][m] = wave_sum(acc[r][m]);
         acc[r][m] = 0.f;
       }
+    if constexpr (KW > 1) {
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) part[wave][r][m] = tot[r][m];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          float t = part[grp * KW][r][m];
+#pragma unroll
+          for (int j = 1; j < KW; ++j) t += part[grp * KW + j][r][m];
+          tot[r][m] = t;
+        }
+      __syncthreads();  // part[] is rewritten by the next tile
+    }
+    if (kw != 0) return;
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
-      const int col = gemv_output(tile, wave, p, PW);
+      const int col = gemv_output(tile, grp, p, PW, GROUPS);
       if (col >= outputs) continue;
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
@@ -159,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
     // Every lane's chunks are in range: batches of U x RPW 16-byte loads, all
     // issued before the first is consumed. Memory parallelism comes from the
     // batch size and from the other waves resident on the SIMD.
-    const int NB = KC / (64 * U);
+    const int NB = KC / (64 * U * KW);
     bool first = true;
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
       if (!first) row_ptrs(tile, wr);
@@ -175,11 +210,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream16(wr[r] + (size_t)(b * U + u) * 512);
+            for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream16(wr[r] + (size_t)(b * U + u) * kStep);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int c = (b * U + u) * 64 + lane;
+          const int c = ((b * U + u) * KW + kw) * 64 + lane;
 #pragma unroll
           for (int m = 0; m < MR; ++m) {
             const u32x4_t xv = xs[m * KC + c];
@@ -192,15 +227,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
     }
   } else {
     // Ragged chunk count: per-lane bounds checks.
-    const int C = (KC + 63) >> 6;
+    const int C = (KC + 63) >> 6;  // chunk blocks per row
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
       row_ptrs(tile, wr);
-      for (int j = 0; j < C; ++j) {
+      for (int j = kw; j < C; j += KW) {
         const int c = j * 64 + lane;
         if (c < KC) {
           u32x4_t wv[RPW];
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) wv[r] = load_stream16(wr[r] + (size_t)j * 512);
+          for (int r = 0; r < RPW; ++r) wv[r] = load_stream16(wr[r] + (size_t)(j - kw) * 512);
 #pragma unroll
           for (int m = 0; m < MR; ++m) {
             const u32x4_t xv = xs[m * KC + c];
@@ -259,54 +294,85 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const uint16_t* 
 
 typedef void (*GemvKernel)(ProjArgs, int);
 
-#define FTK_GEMV_RU(MR, PRO, EPI)                                                             \
-  if (rpw == 2 && unroll == 4) return gemv_kernel<MR, 2, 4, PRO, EPI>;                        \
-  if (rpw == 4 && unroll == 2) return gemv_kernel<MR, 4, 2, PRO, EPI>;                        \
-  if (rpw == 4 && unroll == 4) return gemv_kernel<MR, 4, 4, PRO, EPI>;                        \
-  if (rpw == 8 && unroll == 1) return gemv_kernel<MR, 8, 1, PRO, EPI>;                        \
-  if (rpw == 8 && unroll == 2) return gemv_kernel<MR, 8, 2, PRO, EPI>;                        \
-  return nullptr;
+// Instantiated launch shapes: (rows per group, unroll, waves per group).
+#define FTK_GEMV_SHAPES(MR, PRO, EPI)   \
+  FTK_GEMV_SHAPE(MR, 2, 4, 1, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 4, 2, 1, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 4, 4, 1, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 8, 1, 1, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 8, 2, 1, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 1, 1, 2, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 2, 1, 2, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 1, 2, 2, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 2, 2, 2, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 2, 4, 2, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 1, 1, 4, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 2, 1, 4, PRO, EPI) \
+  FTK_GEMV_SHAPE(MR, 2, 2, 4, PRO, EPI)
 
-#define FTK_GEMV_EPI(MR, PRO)                         \
-  switch (epi) {                                      \
-    case EPI_STORE: { FTK_GEMV_RU(MR, PRO, EPI_STORE) } \
-    case EPI_SWIGLU: { FTK_GEMV_RU(MR, PRO, EPI_SWIGLU) } \
-    case EPI_ARGMAX: { FTK_GEMV_RU(MR, PRO, EPI_ARGMAX) } \
-  }                                                   \
-  return nullptr;
+#define FTK_GEMV_SHAPE(MR, R, U, KW, PRO, EPI) \
+  if (rpw == R && unroll == U && kw == KW) return gemv_kernel<MR, R, U, KW, PRO, EPI>;
+
+template <int MR, bool PRO, int EPI>
+static GemvKernel pick_shape(int rpw, int unroll, int kw) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    // A SwiGLU row group needs a gate row and its up row: even RPW only.
+    if (rpw % 2) return nullptr;
+    if (rpw == 2 && unroll == 4 && kw == 1) return gemv_kernel<MR, 2, 4, 1, PRO, EPI>;
+    if (rpw == 4 && unroll == 2 && kw == 1) return gemv_kernel<MR, 4, 2, 1, PRO, EPI>;
+    if (rpw == 4 && unroll == 4 && kw == 1) return gemv_kernel<MR, 4, 4, 1, PRO, EPI>;
+    if (rpw == 8 && unroll == 1 && kw == 1) return gemv_kernel<MR, 8, 1, 1, PRO, EPI>;
+    if (rpw == 8 && unroll == 2 && kw == 1) return gemv_kernel<MR, 8, 2, 1, PRO, EPI>;
+    if (rpw == 2 && unroll == 1 && kw == 2) return gemv_kernel<MR, 2, 1, 2, PRO, EPI>;
+    if (rpw == 2 && unroll == 2 && kw == 2) return gemv_kernel<MR, 2, 2, 2, PRO, EPI>;
+    if (rpw == 2 && unroll == 4 && kw == 2) return gemv_kernel<MR, 2, 4, 2, PRO, EPI>;
+    if (rpw == 2 && unroll == 1 && kw == 4) return gemv_kernel<MR, 2, 1, 4, PRO, EPI>;
+    if (rpw == 2 && unroll == 2 && kw == 4) return gemv_kernel<MR, 2, 2, 4, PRO, EPI>;
+    return nullptr;
+  } else {
+    FTK_GEMV_SHAPES(MR, PRO, EPI)
+    return nullptr;
+  }
+}
+#undef FTK_GEMV_SHAPE
 
 template <int MR>
-static GemvKernel pick_mr(int rpw, int unroll, bool pro, int epi) {
-  if (pro) {
-    FTK_GEMV_EPI(MR, true)
-  } else {
-    FTK_GEMV_EPI(MR, false)
-  }
-}
-
-static GemvKernel pick_gemv(int M, int rpw, int unroll, bool pro, int epi) {
-  switch (M) {
-    case 1: return pick_mr<1>(rpw, unroll, pro, epi);
-    case 2: return pick_mr<2>(rpw, unroll, pro, epi);
-    case 3: return pick_mr<3>(rpw, unroll, pro, epi);
-    case 4: return pick_mr<4>(rpw, unroll, pro, epi);
+static GemvKernel pick_mr(int rpw, int unroll, int kw, bool pro, int epi) {
+  switch (epi) {
+    case EPI_STORE: return pro ? pick_shape<MR, true, EPI_STORE>(rpw, unroll, kw)
+                               : pick_shape<MR, false, EPI_STORE>(rpw, unroll, kw);
+    case EPI_SWIGLU: return pro ? pick_shape<MR, true, EPI_SWIGLU>(rpw, unroll, kw)
+                                : pick_shape<MR, false, EPI_SWIGLU>(rpw, unroll, kw);
+    case EPI_ARGMAX: return pro ? pick_shape<MR, true, EPI_ARGMAX>(rpw, unroll, kw)
+                                : pick_shape<MR, false, EPI_ARGMAX>(rpw, unroll, kw);
   }
   return nullptr;
 }
 
-bool gemv_supported(int M, int rpw, int unroll, int epi) {
-  return pick_gemv(M, rpw, unroll, false, epi) != nullptr;
+static GemvKernel pick_gemv(int M, int rpw, int unroll, int kw, bool pro, int epi) {
+  switch (M) {
+    case 1: return pick_mr<1>(rpw, unroll, kw, pro, epi);
+    case 2: return pick_mr<2>(rpw, unroll, kw, pro, epi);
+    case 3: return pick_mr<3>(rpw, unroll, kw, pro, epi);
+    case 4: return pick_mr<4>(rpw, unroll, kw, pro, epi);
+  }
+  return nullptr;
+}
+
+bool gemv_supported(int M, int rpw, int unroll, int kw, int epi) {
+  return pick_gemv(M, rpw, unroll, kw, false, epi) != nullptr;
 }
 
 hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& s, hipStream_t stream) {
-  GemvKernel k = pick_gemv(a.M, s.rpw, s.unroll, a.gamma != nullptr, epi);
+  GemvKernel k = pick_gemv(a.M, s.rpw, s.unroll, s.kw, a.gamma != nullptr, epi);
   if (k == nullptr) return hipErrorInvalidValue;
-  if (s.lds > 65536) {
+  const size_t lds = s.lds + (a.gamma != nullptr ? (size_t)a.K * 2 : 0);  // + the staged gain
+  if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s.lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k, dim3(s.grid), dim3(kThreads), s.lds, stream, a, s.tiles);
+  hipLaunchKernelGGL(k, dim3(s.grid), dim3(kThreads), lds, stream, a, s.tiles);
   return hipGetLastError();
 }
 

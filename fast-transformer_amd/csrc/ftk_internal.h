@@ -25,8 +25,9 @@ struct ProjArgs {
 
 // Launch shape of the GEMV kind.
 struct GemvShape {
-  int rpw;       // weight rows per wave per tile (even for SwiGLU)
+  int rpw;       // weight rows per row group per tile (even for SwiGLU)
   int unroll;    // 16-byte chunks per lane issued per batch of loads
+  int kw;        // waves per row group, splitting K (1, 2, 4)
   int grid;      // workgroups (grid-stride over tiles)
   int tiles;
   size_t lds;    // dynamic LDS bytes (x staged as BF16)
@@ -40,7 +41,7 @@ struct DeviceInfo {
 };
 DeviceInfo device_info();
 
-bool gemv_supported(int M, int rpw, int unroll, int epi);
+bool gemv_supported(int M, int rpw, int unroll, int kw, int epi);
 hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& shape, hipStream_t stream);
 
 // Launch shape of the MFMA kind.

@@ -27,20 +27,23 @@ enum Epilogue : int {
 
 // ---- M <= 4: HBM-streaming GEMV (one wave owns whole weight rows) --------
 
-// Outputs one wave produces per tile: RPW rows, or RPW/2 gate/up pairs.
+// Outputs one row group produces per tile: RPW rows, or RPW/2 gate/up pairs.
 FTK_HD int gemv_per_wave(int epi, int rpw) { return epi == EPI_SWIGLU ? rpw / 2 : rpw; }
 
 // Output columns: N (store / argmax) or I = N / 2 (SwiGLU pairs).
 FTK_HD int gemv_outputs(int epi, int n_rows) { return epi == EPI_SWIGLU ? n_rows / 2 : n_rows; }
 
-FTK_HD int gemv_tiles(int epi, int n_rows, int rpw) {
-  const int per_tile = kWaves * gemv_per_wave(epi, rpw);
+// Row groups per workgroup: the 4 waves in groups of KW waves that split K.
+FTK_HD int gemv_groups(int kw) { return kWaves / kw; }
+
+FTK_HD int gemv_tiles(int epi, int n_rows, int rpw, int kw) {
+  const int per_tile = gemv_groups(kw) * gemv_per_wave(epi, rpw);
   return (gemv_outputs(epi, n_rows) + per_tile - 1) / per_tile;
 }
 
-// Output column of (tile, wave, slot).
-FTK_HD int gemv_output(int tile, int wave, int slot, int per_wave) {
-  return (tile * kWaves + wave) * per_wave + slot;
+// Output column of (tile, row group, slot).
+FTK_HD int gemv_output(int tile, int group, int slot, int per_group, int groups) {
+  return (tile * groups + group) * per_group + slot;
 }
 
 // Weight row feeding output ``col``: the row itself, or for SwiGLU the gate row

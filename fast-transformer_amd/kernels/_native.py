@@ -36,7 +36,8 @@ class Config(ctypes.Structure):
 
 
 class Plan(ctypes.Structure):
-    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("grid", _int), ("tiles", _int),
+    _fields_ = [("kind", _int), ("rows_per_wave", _int), ("unroll", _int), ("waves", _int), ("grid", _int),
+                ("tiles", _int),
                 ("threads", _int), ("lds_bytes", _i64), ("splits", _int), ("k_slice", _int),
                 ("workspace_bytes", _i64)]
 

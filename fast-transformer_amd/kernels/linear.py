@@ -105,9 +105,10 @@ def _candidates(m, n, k):
         return [None]
     configs = [None]
     if m <= 4:
-        for rpw, unroll in ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)):
-            for gpc in (4, 8):
-                configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc))
+        for rpw, unroll, kw in ((2, 4, 1), (4, 2, 1), (4, 4, 1), (8, 1, 1), (8, 2, 1), (1, 2, 2), (2, 2, 2),
+                                (2, 4, 2), (1, 1, 4), (2, 1, 4), (2, 2, 4)):
+            for gpc in (4, 8, 16):
+                configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc, kw))
     for rows, unroll, waves in ((16, 4, 4), (16, 8, 4), (16, 4, 8), (16, 8, 8), (16, 4, 16), (32, 4, 4),
                                 (32, 8, 4), (32, 4, 8), (32, 8, 8), (32, 4, 16), (64, 2, 4), (64, 4, 4), (64, 2, 8)):
         configs.append(_native.Config(_native.KIND_MFMA, rows, unroll, 0, waves))

@@ -66,13 +66,15 @@ typedef struct ftk_config {
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
                           MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4) */
   int groups_per_cu;   /* GEMV: grid cap = groups_per_cu * CUs (grid-stride beyond); MFMA: unused */
-  int waves;           /* MFMA: waves per workgroup splitting K (4, 8, 16); GEMV: unused (4) */
+  int waves;           /* MFMA: waves per workgroup splitting K (4, 8, 16);
+                          GEMV: waves per row group splitting K (1, 2, 4; a workgroup is 4 waves) */
 } ftk_config;
 
 typedef struct ftk_plan {
   int kind;
   int rows_per_wave;
   int unroll;
+  int waves;                /* MFMA: waves per workgroup; GEMV: waves per row group */
   int grid;                 /* workgroups launched */
   int tiles;                /* row tiles (GEMV: walked grid-stride; MFMA: 64 rows each) */
   int threads;              /* threads per workgroup (64 per wave) */

@@ -63,17 +63,46 @@ def test_model_shapes_match_oracle(cuda, name, m):
     assert within(bf16.to_f32(got_bits), ref.cpu().numpy())
 
 
+GEMV_SHAPES = {1: ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)), 2: ((1, 2), (2, 2), (2, 4)), 4: ((1, 1), (2, 1), (2, 2))}
+
+
 @pytest.mark.parametrize("m", [1, 2, 4])
-def test_launch_shapes_agree_bit_for_bit(cuda, m):
-    """Rows per wave, unroll and grid cap only regroup the same per-lane FP32 sums."""
-    n, k = 1000, 1024
+@pytest.mark.parametrize("kw", [1, 2, 4])
+def test_launch_shapes_agree_bit_for_bit(cuda, m, kw):
+    """For a given K split (waves per row group), rows per group, unroll and grid cap only
+    regroup the same per-lane FP32 sums: bit-equal. Across K splits: tolerance vs the oracle."""
+    n, k = 1000, 2048
     x = seeded((m, k), seed=7, device=cuda)
     w = seeded((n, k), seed=8, scale=0.02, device=cuda)
-    base = L.project(x, w)
-    for rpw, unroll in ((2, 4), (4, 2), (4, 4), (8, 1), (8, 2)):
+    want = path.project(to_bits(x), to_bits(w))
+    base = None
+    for rpw, unroll in GEMV_SHAPES[kw]:
         for gpc in (1, 2, 8):
-            cfg = _native.Config(_native.KIND_GEMV, rpw, unroll, gpc)
-            assert torch.equal(L.project(x, w, cfg), base), cfg
+            got = L.project(x, w, _native.Config(_native.KIND_GEMV, rpw, unroll, gpc, kw))
+            if base is None:
+                base = got
+                assert within(bf16.to_f32(to_bits(got)), bf16.to_f32(want))
+            assert torch.equal(got, base), (rpw, unroll, gpc, kw)
+
+
+@pytest.mark.parametrize("kw", [2, 4])
+def test_split_k_gemv_fused_epilogues(cuda, kw):
+    """K split across the waves of a row group, with the norm prologue, SwiGLU and argmax epilogues."""
+    from kernels import argmax as A
+    from kernels import swiglu as S
+
+    k, i = 1024, 1536
+    x = seeded((1, k), seed=30, device=cuda)
+    g = seeded((k,), seed=31, scale=0.1, shift=1.0, device=cuda)
+    w = seeded((2 * i, k), seed=32, scale=0.02, device=cuda)
+    cfg = _native.Config(_native.KIND_GEMV, 2, 1 if kw == 4 else 2, 8, kw)
+    got = S.gate_up_swiglu(x, w, g, 1e-6, config=cfg)
+    want = path.gate_up_swiglu(to_bits(x), to_bits(w), to_bits(g), 1e-6)
+    assert within(bf16.to_f32(to_bits(got)), bf16.to_f32(want))
+    got = L.rms_norm_linear(x, g, 1e-6, w, config=cfg)
+    assert within(bf16.to_f32(to_bits(got)), bf16.to_f32(path.norm_project(to_bits(x), to_bits(g), 1e-6, to_bits(w))))
+    ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=cfg)
+    assert int(ids[0]) == int(path.argmax_first(to_bits(logits))[0])
 
 
 def test_generic_kind_for_unaligned_input(cuda):

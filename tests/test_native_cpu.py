@@ -87,7 +87,9 @@ def _coverage(plan, n, epilogue):
 
 def _configs(m):
     if m <= 4:
-        gemv = [_native.Config(_native.KIND_GEMV, rpw, u, gpc) for rpw, u in ((2, 4), (4, 2), (8, 1)) for gpc in (1, 8)]
+        gemv = [_native.Config(_native.KIND_GEMV, rpw, u, gpc, kw)
+                for rpw, u, kw in ((2, 4, 1), (4, 2, 1), (8, 1, 1), (1, 2, 2), (2, 2, 2), (1, 1, 4), (2, 2, 4))
+                for gpc in (1, 8)]
     else:
         gemv = []
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
@@ -104,9 +106,9 @@ def test_plan_writes_every_output_once(m, n, k):
         for cfg in _configs(m):
             if cfg is not None and k % 8:
                 continue
-            if (cfg is not None and cfg.kind == _native.KIND_MFMA and cfg.rows_per_wave == 16
-                    and epilogue == _native.EPI_SWIGLU):
-                continue  # a SwiGLU workgroup needs a gate and an up subtile
+            if (cfg is not None and epilogue == _native.EPI_SWIGLU
+                    and cfg.rows_per_wave in ((16,) if cfg.kind == _native.KIND_MFMA else (1,))):
+                continue  # a SwiGLU workgroup / row group needs a gate row and its up row
             p = _native.Plan()
             status = _native.lib().ftk_plan_project(m, n, k, epilogue, 256, cfg, p)
             if k % 8 and epilogue != _native.EPI_STORE:
