@@ -208,6 +208,14 @@ def cpu_baseline(model, step, budget_s):
             "us_per_layer": round(us, 1)}
 
 
+def kernel_name(plan, prologue, epilogue):
+    """The device function a plan launches, as rocprofv3 lists it (template arguments in order)."""
+    kinds = {_native.KIND_STREAM: "stream_kernel<MR=1, RPW={p.rows_per_wave}, C={p.unroll}, KW={p.waves}",
+             _native.KIND_GEMV: "gemv_kernel<MR=1, RPW={p.rows_per_wave}, U={p.unroll}, KW={p.waves}"}
+    head = kinds.get(plan.kind, "kind {p.kind}<").format(p=plan)
+    return f"ftk::{head}, PRO={int(prologue)}, {epilogue}> grid {plan.grid}"
+
+
 def load_traffic():
     f = ROOT / "profiles" / "traffic_gate_up_swiglu_8b_m1.json"
     if f.exists():
@@ -270,7 +278,8 @@ def main():
     gu_bytes = lb["gate_up"]
     roofline = {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
-                "kernel": "gemv_kernel<1,RPW,U,PRO=1,SWIGLU> (Qwen3-8B gate/up 4096->2x12288, M=1)",
+                "kernel": kernel_name(L.plan(1, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU), True,
+                                      "SWIGLU") + " (Qwen3-8B gate/up 4096->2x12288, M=1)",
                 "avg_launch_us": round(gu_us, 3)}
 
     per_shape = {}

@@ -65,6 +65,32 @@ static GemvDefault gemv_default(int epi, int64_t N, int64_t K) {
   if (!gemv_supported(1, d.rpw, d.unroll, d.kw, epi)) d = {2, 4, 1};  // always instantiated
   return d;
 }
+// STREAM launch shape, from the M = 1 sweep of the Qwen3 shapes on MI355X: the
+// widest K split whose chunk count is instantiated; 4 rows per group for long
+// outputs with short rows (QKV, gate/up, lm_head), else 2.
+struct StreamDefault {
+  int rpw, kw;
+};
+static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
+  if (M < 1 || M > 4 || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  for (int kw : {4, 2, 1}) {
+    const int c = stream_chunks((int)K, kw);
+    if (c == 0) continue;
+    const int want = (c <= 2 && gemv_outputs(epi, (int)N) >= 6144) ? 4 : 2;
+    for (int rpw : {want, 2, 4, 8})
+      if (stream_supported((int)M, rpw, (int)K, kw, epi)) return {rpw, kw};
+  }
+  return {0, 0};
+}
+// STREAM grid cap: small projections run best as ~2 workgroups per CU walking
+// several tiles (the prologue is paid once per workgroup), mid-size ones one
+// tile per workgroup, the largest (lm_head) as deep walks of kStreamMaxTiles.
+static int64_t stream_default_cap(int tiles, int cus) {
+  if (tiles <= 4096) return 2LL * cus;
+  if (tiles <= 16384) return 32LL * cus;
+  return 0;  // the depth limit sets the grid
+}
+
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
 
@@ -77,7 +103,14 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (epi < FTK_EPI_STORE || epi > FTK_EPI_ARGMAX) return FTK_ERR_INVALID;
   if (epi == FTK_EPI_SWIGLU && (N % 2)) return FTK_ERR_INVALID;
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
-  if (kind == FTK_KIND_AUTO) kind = K % 8 ? FTK_KIND_GENERIC : M <= 4 ? FTK_KIND_GEMV : FTK_KIND_MFMA;
+  if (kind == FTK_KIND_AUTO) {
+    if (K % 8)
+      kind = FTK_KIND_GENERIC;
+    else if (M <= 4)
+      kind = stream_default(M, epi, N, K).rpw ? FTK_KIND_STREAM : FTK_KIND_GEMV;
+    else
+      kind = FTK_KIND_MFMA;
+  }
   p->kind = kind;
   p->threads = kThreads;
   p->splits = 1;
@@ -110,6 +143,28 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->lds_bytes = M * K * 2;  // + K * 2 for the staged gain when the prologue is on
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     if (p->lds_bytes + K * 2 > 160 * 1024) return FTK_ERR_UNSUPPORTED;
+    return FTK_OK;
+  }
+  if (kind == FTK_KIND_STREAM) {
+    if (M > 4) return FTK_ERR_UNSUPPORTED;
+    const StreamDefault d = stream_default(M, epi, N, K);
+    const int kw = cfg && cfg->waves ? cfg->waves : d.kw;
+    const int rpw = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : d.rpw;
+    const int c = stream_chunks((int)K, kw);
+    if (c == 0) return FTK_ERR_UNSUPPORTED;  // K is not 512 C KW
+    if (!stream_supported((int)M, rpw, (int)K, kw, epi)) return FTK_ERR_INVALID;
+    p->rows_per_wave = rpw;
+    p->unroll = c;
+    p->waves = kw;
+    p->tiles = gemv_tiles(epi, (int)N, rpw, kw);
+    // Fewest workgroups that keep every walk at the same depth, and no deeper than
+    // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
+    const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
+                                                  : stream_default_cap(p->tiles, cus);
+    const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
+    const int64_t units = cap > floor ? cap : floor;
+    p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     return FTK_OK;
   }
   if (kind == FTK_KIND_MFMA) {
@@ -219,7 +274,9 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
     }
     return FTK_OK;
   }
-  if (p->kind != FTK_KIND_GEMV) return FTK_ERR_UNSUPPORTED;
+  if (p->kind != FTK_KIND_GEMV && p->kind != FTK_KIND_STREAM) return FTK_ERR_UNSUPPORTED;
+  if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
+  if (p->kind == FTK_KIND_STREAM && (p->tiles + p->grid - 1) / p->grid > kStreamMaxTiles) return FTK_ERR_INVALID;
   const int pw = gemv_per_wave(epilogue, p->rows_per_wave);
   const int groups = gemv_groups(p->waves);
   const int halves = epilogue == FTK_EPI_SWIGLU ? 2 : 1;
@@ -277,7 +334,10 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   hipError_t e;
-  if (p.kind == FTK_KIND_GEMV) {
+  if (p.kind == FTK_KIND_STREAM) {
+    StreamShape g = {p.rows_per_wave, p.waves, p.grid, p.tiles};
+    e = launch_stream(a, epilogue, g, s);
+  } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);
   } else {

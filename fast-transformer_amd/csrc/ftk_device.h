@@ -56,6 +56,40 @@ __device__ __forceinline__ float dot8(u32x4_t w, u32x4_t x, float acc) {
   return acc;
 }
 
+// ss + the squares of 8 BF16 values, in element order. Every RMSNorm prologue
+// accumulates through this function, so all kernels scale a row identically.
+__device__ __forceinline__ float sum_squares8(u32x4_t v, float ss) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
+    ss += lo * lo;
+    ss += hi * hi;
+  }
+  return ss;
+}
+
+// RMSNorm of 8 BF16 values: bf16(bf16(x * scale) * gain), the cast order of
+// engine/kernels/rmsnorm.py:35-46.
+__device__ __forceinline__ u32x4_t norm8(u32x4_t v, u32x4_t g, float scale) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+  const uint32_t ge[4] = {g[0], g[1], g[2], g[3]};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float nlo = round_bf16(lo_f32(e[i]) * scale);
+    const float nhi = round_bf16(hi_f32(e[i]) * scale);
+    o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// rsqrt(mean + eps) from the four wave totals of a workgroup, summed in wave order.
+__device__ __forceinline__ float rms_scale(const float (&red)[4], int K, float eps) {
+  const float total = ((red[0] + red[1]) + red[2]) + red[3];
+  return 1.0f / sqrtf(total / (float)K + eps);
+}
+
 // Streaming 16-byte load: weights are read exactly once per call.
 __device__ __forceinline__ u32x4_t load_stream16(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

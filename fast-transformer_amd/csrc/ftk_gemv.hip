@@ -33,7 +33,7 @@ namespace ftk {
 template <int MR, int RPW, int U, int KW, bool PRO, int EPI>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
   extern __shared__ u32x4_t xs[];  // x as [MR][K/8] chunks of 8 BF16 (+ the gain when PRO)
-  __shared__ float red[kWaves][MR];
+  __shared__ float red[MR][kWaves];
   __shared__ float part[kWaves][RPW][MR];
   __shared__ unsigned long long best_lds[kWaves][MR];
 
@@ -92,44 +92,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
     for (int c = tid; c < KC; c += kThreads) {
       const u32x4_t v = load16(a.x + (size_t)m * K + (size_t)c * 8);
       xs[m * KC + c] = v;
-      if constexpr (PRO) {
-        const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
-          ss[m] += lo * lo;
-          ss[m] += hi * hi;
-        }
-      }
+      if constexpr (PRO) ss[m] = sum_squares8(v, ss[m]);
     }
   }
   if constexpr (PRO) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float s = wave_sum(ss[m]);
-      if (lane == 0) red[wave][m] = s;
+      if (lane == 0) red[m][wave] = s;
     }
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       // Same fixed order in every workgroup: every workgroup normalises identically.
-      const float total = ((red[0][m] + red[1][m]) + red[2][m]) + red[3][m];
-      const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
-      for (int c = tid; c < KC; c += kThreads) {
-        const u32x4_t v = xs[m * KC + c];
-        const u32x4_t g = gs[c];
-        const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
-        const uint32_t ge[4] = {g[0], g[1], g[2], g[3]};
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // bf16(x * rsqrt) first, then the gain multiply, rounded again.
-          const float nlo = round_bf16(lo_f32(e[i]) * scale);
-          const float nhi = round_bf16(hi_f32(e[i]) * scale);
-          o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
-        }
-        xs[m * KC + c] = u32x4_t{o[0], o[1], o[2], o[3]};
-      }
+      const float scale = rms_scale(red[m], K, a.eps);
+      for (int c = tid; c < KC; c += kThreads) xs[m * KC + c] = norm8(xs[m * KC + c], gs[c], scale);
     }
   }
   __syncthreads();

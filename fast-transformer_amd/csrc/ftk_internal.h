@@ -44,6 +44,16 @@ DeviceInfo device_info();
 bool gemv_supported(int M, int rpw, int unroll, int kw, int epi);
 hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& shape, hipStream_t stream);
 
+// Launch shape of the STREAM kind (K = 512 C KW, C chunks per lane per row).
+struct StreamShape {
+  int rpw;       // weight rows per row group per tile (even for SwiGLU)
+  int kw;        // waves per row group, splitting K (1, 2, 4)
+  int grid;      // workgroups; each walks ceil(tiles / grid) <= kStreamMaxTiles tiles
+  int tiles;
+};
+bool stream_supported(int M, int rpw, int K, int kw, int epi);
+hipError_t launch_stream(const ProjArgs& a, int epi, const StreamShape& shape, hipStream_t stream);
+
 // Launch shape of the MFMA kind.
 struct MfmaShape {
   int subtiles;  // T: 16-row MFMA subtiles per workgroup

@@ -40,23 +40,11 @@ __global__ __launch_bounds__(kThreads) void row_scale_kernel(const uint16_t* __r
   const int KC = K >> 3;
   const uint16_t* xr = x + (size_t)blockIdx.x * K;
   float ss = 0.f;
-  for (int c = tid; c < KC; c += kThreads) {
-    const u32x4_t v = load16(xr + (size_t)c * 8);
-    const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
-      ss += lo * lo;
-      ss += hi * hi;
-    }
-  }
+  for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(xr + (size_t)c * 8), ss);
   const float s = wave_sum(ss);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (tid == 0) {
-    const float total = ((red[0] + red[1]) + red[2]) + red[3];
-    scale[blockIdx.x] = 1.0f / sqrtf(total / (float)K + eps);
-  }
+  if (tid == 0) scale[blockIdx.x] = rms_scale(red, K, eps);
 }
 
 template <int MB, int T, int U, int W, int EPI, bool PRO>

@@ -52,6 +52,16 @@ FTK_HD int gemv_weight_row(int epi, int col, int half, int n_rows) {
   return epi == EPI_SWIGLU ? col + half * (n_rows / 2) : col;
 }
 
+// ---- M <= 4 with K = 512 C KW: the STREAM kind (x slice in registers) ------
+// Same tiles, row groups and weight rows as the GEMV kind above. Workgroup b
+// walks tiles b, b + grid, ... (at most kStreamMaxTiles of them) and lane l of
+// wave kw of a row group owns the K chunks (j KW + kw) 64 + l, j < C.
+
+constexpr int kStreamMaxTiles = 8;  // tiles per workgroup: their wave totals wait in LDS
+
+// 16-byte chunks per lane per weight row (C), or 0 when K is not 512 C KW.
+FTK_HD int stream_chunks(int k, int kw) { return (kw < 1 || k % (512 * kw)) ? 0 : k / (512 * kw); }
+
 // ---- M >= 4: BF16 MFMA skinny GEMM (T subtiles of 16 weight rows per workgroup)
 
 constexpr int kMfmaK = 32;          // K per MFMA step (v_mfma_f32_16x16x32_bf16)

@@ -1,0 +1,267 @@
+// M = 1..4 skinny BF16 projection, STREAM kind: an HBM-streaming GEMV whose
+// x slice lives in registers, for K = 512 C KW (every model shape of the path).
+//
+// Same sums, roundings and fused extras as the GEMV kind (engine/kernels/linear.py:27-47
+// _gemv; RMSNorm prologue engine/kernels/rmsnorm.py:21-46; SwiGLU epilogue
+// engine/kernels/swiglu.py:13-24; greedy-argmax epilogue engine/kernels/argmax.py:19-48),
+// and for the same (rows per group, KW) the same FP32 sums bit for bit: lane l of
+// wave kw accumulates chunks (j KW + kw) 64 + l in j order, the DPP tree sums the
+// lanes, the KW wave totals are added in wave order.
+//
+// What differs is the schedule, built to keep HBM busy from the first cycle to
+// the last:
+//   * Lane l only ever multiplies its own C chunks of K, so it loads those chunks
+//     of x (normalised in registers when the prologue is on) once, and never
+//     touches LDS in the main loop.
+//   * Rolling prefetch: as each weight chunk of tile i is consumed, the load of
+//     the same chunk of tile i + 1 is issued into the register it frees, so a
+//     wave keeps RPW x C 16-byte loads in flight through its whole life.
+//   * The first tile's loads are issued before x is read and normalised.
+//   * No barrier inside the tile loop: each wave's per-tile totals wait in LDS,
+//     and one barrier at the end lets all 256 threads combine the KW totals and
+//     run the epilogue for every output of the workgroup.
+#include "ftk_device.h"
+#include "ftk_internal.h"
+
+namespace ftk {
+
+template <int MR, int RPW, int C, int KW, bool PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles) {
+  constexpr int GROUPS = kWaves / KW;
+  constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per row group per tile
+  constexpr size_t kStep = (size_t)KW * 512;                // elements between a lane's chunks
+  __shared__ float part[kStreamMaxTiles][kWaves][RPW][MR];  // wave totals per tile
+  __shared__ float red[MR][kWaves];
+  __shared__ unsigned long long best_lds[kWaves][MR];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave / KW, kw = wave - grp * KW;
+  const int K = a.K;  // == 512 C KW (checked by the planner)
+  const int outputs = gemv_outputs(EPI, a.N);
+  const size_t first = (size_t)(kw * 64 + lane) * 8;  // this lane's chunk j = 0
+
+  auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int col = gemv_output(tile, grp, p, PW, GROUPS);
+      const int c = col < outputs ? col : outputs - 1;  // clamp: loads stay in bounds
+      wr[p] = a.w + (size_t)gemv_weight_row(EPI, c, 0, a.N) * K + first;
+      if constexpr (EPI == EPI_SWIGLU) wr[PW + p] = a.w + (size_t)gemv_weight_row(EPI, c, 1, a.N) * K + first;
+    }
+  };
+
+  // ---- this lane's slice of x (and of the gain): small, mostly cache hits ---
+  // Issued first: loads complete in issue order, so the prologue below waits
+  // for these and not for the weight batch issued after them.
+  u32x4_t xr[MR][C];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < C; ++j) xr[m][j] = load16(a.x + (size_t)m * K + first + j * kStep);
+  u32x4_t g[PRO ? C : 1];
+  if constexpr (PRO) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) g[j] = load16(a.gamma + first + j * kStep);
+  }
+
+  // ---- first tile's weights in flight before the prologue -------------------
+  int tile = blockIdx.x;  // grid <= tiles
+  const uint16_t* wr[RPW];
+  row_ptrs(tile, wr);
+  u32x4_t wv[C][RPW];
+#pragma unroll
+  for (int j = 0; j < C; ++j)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) wv[j][r] = load_stream16(wr[r] + j * kStep);
+
+  // ---- RMSNorm prologue: normalise the slice in registers -------------------
+  if constexpr (PRO) {
+    // Sum of squares in the thread order of the other kinds' prologues
+    // (thread t: chunks t, t + 256, ...), so every kind scales a row alike.
+    // With KW = 4 thread t's own chunks (4 j + wave) 64 + lane are exactly
+    // those, in that order; otherwise re-read x in that order.
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float ss = 0.f;
+      if constexpr (KW == kWaves) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) ss = sum_squares8(xr[m][j], ss);
+      } else {
+        const int KC = K >> 3;
+        for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(a.x + (size_t)m * K + (size_t)c * 8), ss);
+      }
+      const float s = wave_sum(ss);
+      if (lane == 0) red[m][wave] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float scale = rms_scale(red[m], K, a.eps);
+#pragma unroll
+      for (int j = 0; j < C; ++j) xr[m][j] = norm8(xr[m][j], g[j], scale);
+    }
+  }
+
+  // ---- tiles: consume, prefetch the next tile chunk by chunk, park the totals
+  int count = 0;
+  for (;;) {
+    const int next = tile + (int)gridDim.x;
+    float acc[RPW][MR];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+    if (next < tiles) {
+      const uint16_t* wn[RPW];
+      row_ptrs(next, wn);
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          // Consume, then reload the same register: the new load never has to
+          // live beside the old value, so it needs no copy at the loop edge.
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[r][m] = dot8(wv[j][r], xr[m][j], acc[r][m]);
+          wv[j][r] = load_stream16(wn[r] + j * kStep);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) acc[r][m] = dot8(wv[j][r], xr[m][j], acc[r][m]);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float t = wave_sum(acc[r][m]);
+        if (lane == 0) part[count][wave][r][m] = t;
+      }
+    ++count;
+    if (next >= tiles) break;
+    tile = next;
+  }
+  __syncthreads();
+
+  // ---- epilogue: every thread takes outputs (tile i, group, slot) ------------
+  unsigned long long best[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) best[m] = 0ull;
+  const int entries = count * GROUPS * PW;  // count is the same in every wave of the workgroup
+  for (int e = tid; e < entries; e += kThreads) {
+    const int p = e % PW;
+    const int g = (e / PW) % GROUPS;
+    const int i = e / (PW * GROUPS);
+    const int col = gemv_output(blockIdx.x + i * (int)gridDim.x, g, p, PW, GROUPS);
+    if (col >= outputs) continue;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float s = part[i][g * KW][p][m];
+#pragma unroll
+      for (int k = 1; k < KW; ++k) s += part[i][g * KW + k][p][m];
+      if constexpr (EPI == EPI_STORE) {
+        a.y[(size_t)m * a.N + col] = (uint16_t)f32_to_bf16(s);
+      } else if constexpr (EPI == EPI_SWIGLU) {
+        float u = part[i][g * KW][PW + p][m];
+#pragma unroll
+        for (int k = 1; k < KW; ++k) u += part[i][g * KW + k][PW + p][m];
+        a.y[(size_t)m * (a.N / 2) + col] = (uint16_t)swiglu_bf16(s, u);
+      } else {
+        const uint32_t bits = f32_to_bf16(s);
+        if (a.y != nullptr) a.y[(size_t)m * a.N + col] = (uint16_t)bits;
+        best[m] = key_max(best[m], argmax_key(bf16_to_f32(bits), (uint32_t)col));
+      }
+    }
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    // This workgroup's best key per input row; the finalize pass reduces the workgroups.
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) best[m] = key_max(best[m], __shfl_xor(best[m], off));
+      if (lane == 0) best_lds[wave][m] = best[m];
+    }
+    __syncthreads();
+    if (tid < MR) {
+      unsigned long long k = best_lds[0][tid];
+      for (int w = 1; w < kWaves; ++w) k = key_max(k, best_lds[w][tid]);
+      a.keys[(size_t)blockIdx.x * MR + tid] = k;
+    }
+  }
+}
+
+// ---- dispatch -------------------------------------------------------------------
+
+typedef void (*StreamKernel)(ProjArgs, int);
+
+// Instantiated (rows per group, C, KW): the K of each model shape of the path
+// (1024, 2048, 3072, 4096, 12288) with two or three row-group sizes each.
+#define FTK_STREAM_SHAPES(MR, PRO, EPI)   \
+  FTK_STREAM_SHAPE(MR, 2, 1, 2, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 4, 1, 2, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 8, 1, 2, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 2, 1, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 4, 1, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 2, 3, 2, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 4, 3, 2, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 2, 2, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 4, 2, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 8, 2, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 2, 6, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 4, 6, 4, PRO, EPI)
+
+#define FTK_STREAM_SHAPE(MR, R, CC, KW, PRO, EPI) \
+  if (rpw == R && c == CC && kw == KW) return stream_kernel<MR, R, CC, KW, PRO, EPI>;
+
+template <int MR, bool PRO, int EPI>
+static StreamKernel pick_stream_shape(int rpw, int c, int kw) {
+  FTK_STREAM_SHAPES(MR, PRO, EPI)
+  return nullptr;
+}
+#undef FTK_STREAM_SHAPE
+
+template <int MR>
+static StreamKernel pick_stream_mr(int rpw, int c, int kw, bool pro, int epi) {
+  switch (epi) {
+    case EPI_STORE: return pro ? pick_stream_shape<MR, true, EPI_STORE>(rpw, c, kw)
+                               : pick_stream_shape<MR, false, EPI_STORE>(rpw, c, kw);
+    case EPI_SWIGLU: return pro ? pick_stream_shape<MR, true, EPI_SWIGLU>(rpw, c, kw)
+                                : pick_stream_shape<MR, false, EPI_SWIGLU>(rpw, c, kw);
+    case EPI_ARGMAX: return pro ? pick_stream_shape<MR, true, EPI_ARGMAX>(rpw, c, kw)
+                                : pick_stream_shape<MR, false, EPI_ARGMAX>(rpw, c, kw);
+  }
+  return nullptr;
+}
+
+static StreamKernel pick_stream(int M, int rpw, int c, int kw, bool pro, int epi) {
+  switch (M) {
+    case 1: return pick_stream_mr<1>(rpw, c, kw, pro, epi);
+    case 2: return pick_stream_mr<2>(rpw, c, kw, pro, epi);
+    case 3: return pick_stream_mr<3>(rpw, c, kw, pro, epi);
+    case 4: return pick_stream_mr<4>(rpw, c, kw, pro, epi);
+  }
+  return nullptr;
+}
+
+bool stream_supported(int M, int rpw, int K, int kw, int epi) {
+  const int c = stream_chunks(K, kw);
+  return c > 0 && pick_stream(M, rpw, c, kw, false, epi) != nullptr;
+}
+
+hipError_t launch_stream(const ProjArgs& a, int epi, const StreamShape& s, hipStream_t stream) {
+  const int c = stream_chunks(a.K, s.kw);
+  StreamKernel k = c > 0 ? pick_stream(a.M, s.rpw, c, s.kw, a.gamma != nullptr, epi) : nullptr;
+  if (k == nullptr) return hipErrorInvalidValue;
+  // Every workgroup walks at most kStreamMaxTiles tiles (their totals wait in LDS).
+  if (s.grid < 1 || s.grid > s.tiles || (s.tiles + s.grid - 1) / s.grid > kStreamMaxTiles)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(s.grid), dim3(kThreads), 0, stream, a, s.tiles);
+  return hipGetLastError();
+}
+
+}  // namespace ftk

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).with_name("libftk.so")
 
 FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = range(5)
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
-KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC = range(4)
+KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM = range(5)
 MAX_ROWS = 32
 
 _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float

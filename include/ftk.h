@@ -54,7 +54,9 @@ typedef enum ftk_kind {
   FTK_KIND_AUTO = 0,
   FTK_KIND_GEMV = 1,     /* M <= 4: HBM-streaming GEMV (v_dot2_f32_bf16, LDS-resident x) */
   FTK_KIND_MFMA = 2,     /* M >= 4: v_mfma_f32_16x16x32_bf16 tiles */
-  FTK_KIND_GENERIC = 3   /* any shape/alignment, scalar loads; store epilogue only */
+  FTK_KIND_GENERIC = 3,  /* any shape/alignment, scalar loads; store epilogue only */
+  FTK_KIND_STREAM = 4    /* M <= 4, K = 512 C KW: HBM-streaming GEMV, x slice in registers,
+                            rolling weight prefetch, one barrier per workgroup */
 } ftk_kind;
 
 /* Launch choice for one projection (the reference's per-shape config tuple,
@@ -62,12 +64,15 @@ typedef enum ftk_kind {
  * Zero fields mean "planner default". */
 typedef struct ftk_config {
   int kind;            /* ftk_kind */
-  int rows_per_wave;   /* GEMV: weight rows per wave per tile (2, 4, 8); MFMA: rows per workgroup (16, 32, 64) */
+  int rows_per_wave;   /* GEMV, STREAM: weight rows per row group per tile (1..8);
+                          MFMA: rows per workgroup (16, 32, 64) */
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
-                          MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4) */
-  int groups_per_cu;   /* GEMV: grid cap = groups_per_cu * CUs (grid-stride beyond); MFMA: unused */
+                          MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4);
+                          STREAM: unused (K fixes the chunks per lane) */
+  int groups_per_cu;   /* GEMV, STREAM: grid cap = groups_per_cu * CUs (grid-stride beyond; STREAM
+                          raises the grid so no workgroup walks more than 8 tiles); MFMA: unused */
   int waves;           /* MFMA: waves per workgroup splitting K (4, 8, 16);
-                          GEMV: waves per row group splitting K (1, 2, 4; a workgroup is 4 waves) */
+                          GEMV, STREAM: waves per row group splitting K (1, 2, 4; a workgroup is 4 waves) */
 } ftk_config;
 
 typedef struct ftk_plan {

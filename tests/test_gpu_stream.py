@@ -1,0 +1,122 @@
+"""GPU parity of the STREAM kind (x slice in registers, rolling weight prefetch).
+
+For the same K split (KW waves per row group) the STREAM kind adds the same FP32
+products in the same order as the GEMV kind: per lane in chunk order, the DPP
+tree over lanes, the KW wave totals in wave order; its RMSNorm prologue sums
+squares in the other kinds' thread order. So STREAM output must equal the GEMV
+kind's bit for bit, for every epilogue, with and without the prologue, for every
+grid depth (1..8 tiles per workgroup). Against the CPU oracle the bar is
+|y - ref| <= 2e-2 + 1e-2|ref| and bit-exact argmax ids.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import seeded, to_bits
+from oracle import bf16, path
+
+from kernels import _native
+from kernels import argmax as A
+from kernels import linear as L
+from kernels import swiglu as S
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+#: (rows per group, chunks per lane C, KW): the instantiated STREAM shapes (K = 512 C KW).
+STREAM_SHAPES = ((2, 1, 2), (4, 1, 2), (8, 1, 2), (2, 1, 4), (4, 1, 4), (2, 3, 2), (4, 3, 2), (2, 2, 4), (4, 2, 4),
+                 (8, 2, 4), (2, 6, 4), (4, 6, 4))
+
+
+def within(got_bits, want_bits):
+    g, w = bf16.to_f32(got_bits).astype(np.float64), bf16.to_f32(want_bits).astype(np.float64)
+    return bool(np.all(np.abs(g - w) <= ATOL + RTOL * np.abs(w)))
+
+
+def stream(rpw, kw, gpc=0):
+    return _native.Config(_native.KIND_STREAM, rpw, 0, gpc, kw)
+
+
+def gemv(kw):
+    # Any GEMV launch shape with the same KW adds in the same order; (2, 1, KW) exists for KW 2 and 4.
+    return _native.Config(_native.KIND_GEMV, 2, 1 if kw > 1 else 4, 0, kw)
+
+
+def _inputs(m, n, k, seed, device):
+    x = seeded((m, k), seed=seed, device=device)
+    w = seeded((n, k), seed=seed + 1, scale=0.02, device=device)
+    g = seeded((k,), seed=seed + 2, scale=0.1, shift=1.0, device=device)
+    return x, w, g
+
+
+@pytest.mark.parametrize("rpw,c,kw", STREAM_SHAPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_store_equals_gemv_kind_and_oracle(cuda, rpw, c, kw, m):
+    k = 512 * c * kw
+    n = 1000 + 8 * rpw + 3  # ragged last tile
+    x, w, g = _inputs(m, n, k, seed=200 + rpw + 10 * c + m, device=cuda)
+    got = L.project(x, w, stream(rpw, kw))
+    assert torch.equal(got, L.project(x, w, gemv(kw)))
+    assert within(to_bits(got), path.project(to_bits(x), to_bits(w)))
+    normed = L.rms_norm_linear(x, g, 1e-6, w, config=stream(rpw, kw))
+    assert torch.equal(normed, L.rms_norm_linear(x, g, 1e-6, w, config=gemv(kw)))
+    assert within(to_bits(normed), path.norm_project(to_bits(x), to_bits(g), 1e-6, to_bits(w)))
+
+
+@pytest.mark.parametrize("rpw,c,kw", [s for s in STREAM_SHAPES if s[0] % 2 == 0])
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("with_norm", [False, True])
+def test_swiglu_equals_gemv_kind_and_oracle(cuda, rpw, c, kw, m, with_norm):
+    k = 512 * c * kw
+    i = 700 + rpw // 2 + 1
+    x, w, g = _inputs(m, 2 * i, k, seed=300 + rpw + 10 * c + m, device=cuda)
+    g = g if with_norm else None
+    got = S.gate_up_swiglu(x, w, g, 1e-6, config=stream(rpw, kw))
+    assert torch.equal(got, S.gate_up_swiglu(x, w, g, 1e-6, config=gemv(kw)))
+    want = path.gate_up_swiglu(to_bits(x), to_bits(w), None if g is None else to_bits(g), 1e-6)
+    assert within(to_bits(got), want)
+
+
+@pytest.mark.parametrize("rpw,c,kw", [(8, 1, 2), (4, 2, 4), (8, 2, 4), (2, 6, 4)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_argmax_equals_gemv_kind_and_oracle(cuda, rpw, c, kw, m):
+    k = 512 * c * kw
+    v = 20000 + rpw
+    x, w, g = _inputs(m, v, k, seed=400 + rpw + 10 * c + m, device=cuda)
+    ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=stream(rpw, kw))
+    ids_g, logits_g = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=gemv(kw))
+    assert torch.equal(logits, logits_g) and torch.equal(ids, ids_g)
+    want = path.norm_project(to_bits(x), to_bits(g), 1e-6, to_bits(w))
+    assert within(to_bits(logits), want)
+    np.testing.assert_array_equal(ids.cpu().numpy(), path.argmax_first(to_bits(logits)))
+    # without the logits buffer: same ids
+    ids_only, none = A.lm_head_argmax(x, w, g, 1e-6, logits=False, config=stream(rpw, kw))
+    assert none is None and torch.equal(ids_only, ids)
+
+
+@pytest.mark.parametrize("gpc", [1, 2, 3, 8, 64])
+def test_grid_depth_does_not_change_bits(cuda, gpc):
+    """Workgroups walking 1..8 tiles: the per-tile sums do not depend on the walk."""
+    x, w, g = _inputs(2, 24000, 4096, seed=500, device=cuda)
+    base = L.rms_norm_linear(x, g, 1e-6, w, config=stream(4, 4, 64))
+    p = L.plan(2, 24000, 4096, _native.EPI_STORE, config=stream(4, 4, gpc))
+    assert 1 <= -(-p.tiles // p.grid) <= 8
+    assert torch.equal(L.rms_norm_linear(x, g, 1e-6, w, config=stream(4, 4, gpc)), base)
+
+
+def test_argmax_ties_take_lowest_index(cuda):
+    """Duplicate weight rows give exactly tied logits; the lowest index must win across workgroups."""
+    k, v = 4096, 30000
+    x, w, g = _inputs(1, v, k, seed=600, device=cuda)
+    w[29999] = (x[0].float() * 0.05).to(torch.bfloat16)  # aligned with x: a clear winner ...
+    w[15000] = w[29999]  # ... tied with an earlier row in another workgroup
+    ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=stream(4, 4, 1))
+    assert int(ids[0]) == int(path.argmax_first(to_bits(logits))[0])
+    assert logits[0, 15000] == logits[0, 29999] and int(ids[0]) <= 15000
+
+
+def test_default_plan_is_stream_for_model_shapes(cuda):
+    for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288), (4096, 1024), (1024, 2048), (1024, 3072)):
+        assert L.plan(1, n, k).kind == _native.KIND_STREAM, (n, k)

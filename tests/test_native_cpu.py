@@ -85,11 +85,24 @@ def _coverage(plan, n, epilogue):
     return np.frombuffer(counts, dtype=np.int32), max_row.value
 
 
+#: (rows per group, chunks per lane C, KW) the STREAM kind instantiates (K = 512 C KW).
+STREAM_SHAPES = ((2, 1, 2), (4, 1, 2), (8, 1, 2), (2, 1, 4), (4, 1, 4), (2, 3, 2), (4, 3, 2), (2, 2, 4), (4, 2, 4),
+                 (8, 2, 4), (2, 6, 4), (4, 6, 4))
+
+
+def _stream_status(k, rpw, kw):
+    if k % (512 * kw):
+        return _native.FTK_ERR_UNSUPPORTED
+    return _native.FTK_OK if (rpw, k // (512 * kw), kw) in STREAM_SHAPES else _native.FTK_ERR_INVALID
+
+
 def _configs(m):
     if m <= 4:
         gemv = [_native.Config(_native.KIND_GEMV, rpw, u, gpc, kw)
                 for rpw, u, kw in ((2, 4, 1), (4, 2, 1), (8, 1, 1), (1, 2, 2), (2, 2, 2), (1, 1, 4), (2, 2, 4))
                 for gpc in (1, 8)]
+        gemv += [_native.Config(_native.KIND_STREAM, rpw, 0, gpc, kw)
+                 for rpw, _, kw in STREAM_SHAPES for gpc in (1, 8, 16)]
     else:
         gemv = []
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
@@ -114,6 +127,11 @@ def test_plan_writes_every_output_once(m, n, k):
             if k % 8 and epilogue != _native.EPI_STORE:
                 assert status == _native.FTK_ERR_UNSUPPORTED
                 continue
+            if cfg is not None and cfg.kind == _native.KIND_STREAM:
+                want = _stream_status(k, cfg.rows_per_wave, cfg.waves)
+                assert status == want, (m, n, k, epilogue, cfg)
+                if want != _native.FTK_OK:
+                    continue
             assert status == _native.FTK_OK, (m, n, k, epilogue, cfg)
             counts, max_row = _coverage(p, n, epilogue)
             assert np.all(counts == 1), (m, n, k, epilogue, cfg)
@@ -121,6 +139,10 @@ def test_plan_writes_every_output_once(m, n, k):
             if p.kind == _native.KIND_GEMV:
                 assert 1 <= p.grid <= p.tiles
                 assert p.lds_bytes == m * k * 2
+            if p.kind == _native.KIND_STREAM:
+                # every walk equally deep (within one tile) and at most 8 tiles: their totals wait in LDS
+                assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
+                assert p.unroll * 512 * p.waves == k and p.lds_bytes == 0
             if p.kind == _native.KIND_MFMA:
                 # one workgroup per tile over all of K: no split-K, nothing shared between workgroups
                 assert p.grid == p.tiles and p.splits == 1 and p.k_slice == k
@@ -131,7 +153,11 @@ def test_plan_writes_every_output_once(m, n, k):
 def test_plan_kinds():
     p = _native.Plan()
     _native.call("ftk_plan_project", 1, 4096, 4096, 0, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.threads == 256 and p.unroll * 512 * p.waves == 4096
+    _native.call("ftk_plan_project", 1, 4096, 4104, 0, 256, None, p)  # K % 512 != 0: the LDS-staged GEMV
     assert p.kind == _native.KIND_GEMV and p.threads == 256
+    _native.call("ftk_plan_project", 4, 151936, 4096, _native.EPI_ARGMAX, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
     _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
