@@ -72,8 +72,8 @@ struct StreamDefault {
   int rpw, kw;
 };
 static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
-  if (M < 1 || M > 4 || K > INT32_MAX || N > INT32_MAX) return {0, 0};
-  for (int kw : {4, 2, 1}) {
+  if (M < 1 || M > kStreamMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  for (int kw : {4, 2, 1, 8}) {
     const int c = stream_chunks((int)K, kw);
     if (c == 0) continue;
     const int want = (c <= 2 && gemv_outputs(epi, (int)N) >= 6144) ? 4 : 2;
@@ -91,12 +91,35 @@ static int64_t stream_default_cap(int tiles, int cus) {
   return 0;  // the depth limit sets the grid
 }
 
+// MFMA_STREAM launch shape, from the M = 5 / 16 sweep of the Qwen3-8B shapes on
+// MI355X: 8 waves split K (16 steps of 32 at K = 4096) with 8 steps in flight
+// (16 for lm_head); 16 waves and 4 steps for a small projection with the
+// prologue (QKV); two subtiles per tile for SwiGLU (a gate and an up subtile).
+// K = 12288 has only the 16-wave kernel (24 steps), without the prologue.
+struct MstreamDefault {
+  int t, kw, unroll;
+};
+static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
+  if (M < 1 || M > kMstreamMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
+  const int t = epi == FTK_EPI_SWIGLU ? 2 : 1;
+  const bool small_pro = pro && epi == FTK_EPI_STORE && mfma_tiles(epi, (int)N, 1) <= 512;
+  const MstreamDefault order[] = {
+      small_pro ? MstreamDefault{t, 16, 4} : MstreamDefault{t, 8, epi == FTK_EPI_ARGMAX ? 16 : 8},
+      {t, 8, 8}, {t, 8, 4}, {t, 16, 4}, {t, 16, 2}};
+  for (const MstreamDefault& d : order)
+    if (mstream_supported((int)M, d.t, (int)K, d.kw, d.unroll, epi, pro)) return d;
+  return {0, 0, 0};
+}
+
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
 
 static int64_t argmax_keys_bytes(int grid, int64_t M) { return kWsKeys + (int64_t)grid * M * 8; }
 
+// epi may carry FTK_PLAN_PROLOGUE: plan a call with the RMSNorm prologue.
 static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_config* cfg, ftk_plan* p) {
+  const bool pro = (epi & FTK_PLAN_PROLOGUE) != 0;
+  epi &= ~FTK_PLAN_PROLOGUE;
   memset(p, 0, sizeof(*p));
   if (M < 1 || M > FTK_MAX_ROWS || N < 1 || K < 1 || cus < 1) return FTK_ERR_INVALID;
   if (N > INT32_MAX / 2 || K > INT32_MAX / 2) return FTK_ERR_INVALID;
@@ -106,10 +129,22 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (kind == FTK_KIND_AUTO) {
     if (K % 8)
       kind = FTK_KIND_GENERIC;
+    else if (M <= 4 && stream_default(M, epi, N, K).rpw)
+      kind = FTK_KIND_STREAM;
     else if (M <= 4)
-      kind = stream_default(M, epi, N, K).rpw ? FTK_KIND_STREAM : FTK_KIND_GEMV;
-    else
-      kind = FTK_KIND_MFMA;
+      kind = FTK_KIND_GEMV;
+    else {
+      const MstreamDefault d = mstream_default(M, epi, pro, N, K);
+      // K = 12288 (24 MFMA steps per wave) at M <= 8: 8 waves of v_dot2 (the
+      // 8-row STREAM kernel) beat the 16-wave MFMA kernel on MI355X.
+      const bool long_k = d.t && mstream_steps((int)K, d.kw) > 16;
+      if (d.t && !(long_k && M <= kStreamMaxRows && stream_default(M, epi, N, K).rpw))
+        kind = FTK_KIND_MFMA_STREAM;
+      else if (M <= kStreamMaxRows && stream_default(M, epi, N, K).rpw)
+        kind = FTK_KIND_STREAM;
+      else
+        kind = FTK_KIND_MFMA;
+    }
   }
   p->kind = kind;
   p->threads = kThreads;
@@ -146,7 +181,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     return FTK_OK;
   }
   if (kind == FTK_KIND_STREAM) {
-    if (M > 4) return FTK_ERR_UNSUPPORTED;
+    if (M > kStreamMaxRows) return FTK_ERR_UNSUPPORTED;
     const StreamDefault d = stream_default(M, epi, N, K);
     const int kw = cfg && cfg->waves ? cfg->waves : d.kw;
     const int rpw = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : d.rpw;
@@ -156,12 +191,35 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->rows_per_wave = rpw;
     p->unroll = c;
     p->waves = kw;
+    p->threads = 64 * stream_waves(kw);
     p->tiles = gemv_tiles(epi, (int)N, rpw, kw);
     // Fewest workgroups that keep every walk at the same depth, and no deeper than
     // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
                                                   : stream_default_cap(p->tiles, cus);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
+    const int64_t units = cap > floor ? cap : floor;
+    p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
+    return FTK_OK;
+  }
+  if (kind == FTK_KIND_MFMA_STREAM) {
+    if (M > kMstreamMaxRows) return FTK_ERR_UNSUPPORTED;
+    const MstreamDefault d = mstream_default(M, epi, pro, N, K);
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 16 * d.t;
+    const int kw = cfg && cfg->waves ? cfg->waves : d.kw;
+    const int unroll = cfg && cfg->unroll ? cfg->unroll : d.unroll;
+    if (mstream_steps((int)K, kw) == 0) return FTK_ERR_UNSUPPORTED;  // K is not 32 S KW
+    if (rows % 16 || !mstream_supported((int)M, rows / 16, (int)K, kw, unroll, epi, pro)) return FTK_ERR_INVALID;
+    const int t = rows / 16;
+    p->rows_per_wave = rows;
+    p->unroll = unroll;
+    p->waves = kw;
+    p->threads = 64 * kw;
+    p->tiles = mfma_tiles(epi, (int)N, t);
+    const int64_t cap = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
+    const int depth = mstream_max_depth(t, kw);
+    const int64_t floor = (p->tiles + depth - 1) / depth;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
@@ -274,6 +332,26 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
     }
     return FTK_OK;
   }
+  if (p->kind == FTK_KIND_MFMA_STREAM) {
+    // Workgroup b walks tiles b + i grid; a tile is T subtiles of 16 weight rows.
+    const int t = p->rows_per_wave / 16;
+    if (t < 1 || p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
+    if ((p->tiles + p->grid - 1) / p->grid > mstream_max_depth(t, p->waves)) return FTK_ERR_INVALID;
+    const int per = mfma_out_per_tile(epilogue, t);
+    for (int b = 0; b < p->grid; ++b)
+      for (int tile = b; tile < p->tiles; tile += p->grid) {
+        for (int sub = 0; sub < t; ++sub)
+          for (int li = 0; li < 16; ++li) {
+            const int64_t row = mfma_weight_row(epilogue, tile, sub, li, (int)N, t);
+            if (row > *max_row) *max_row = row;
+          }
+        for (int r = 0; r < per; ++r) {
+          const int64_t col = (int64_t)tile * per + r;
+          if (col < outputs) counts[col] += 1;
+        }
+      }
+    return FTK_OK;
+  }
   if (p->kind != FTK_KIND_GEMV && p->kind != FTK_KIND_STREAM) return FTK_ERR_UNSUPPORTED;
   if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
   if (p->kind == FTK_KIND_STREAM && (p->tiles + p->grid - 1) / p->grid > kStreamMaxTiles) return FTK_ERR_INVALID;
@@ -307,7 +385,7 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   DeviceInfo d = device_info();
   if (!d.ok) return hip_status(hipErrorNoDevice);
   ftk_plan p;
-  int st = plan(M, N, K, epilogue, d.cus, cfg, &p);
+  int st = plan(M, N, K, epilogue | (gamma != nullptr ? FTK_PLAN_PROLOGUE : 0), d.cus, cfg, &p);
   if (st != FTK_OK) return st;
   const int64_t need = call_workspace(p, epilogue, gamma != nullptr);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return FTK_ERR_WORKSPACE;
@@ -337,6 +415,9 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   if (p.kind == FTK_KIND_STREAM) {
     StreamShape g = {p.rows_per_wave, p.waves, p.grid, p.tiles};
     e = launch_stream(a, epilogue, g, s);
+  } else if (p.kind == FTK_KIND_MFMA_STREAM) {
+    MstreamShape g = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid, p.tiles};
+    e = launch_mstream(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);

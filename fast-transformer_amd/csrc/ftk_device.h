@@ -90,6 +90,13 @@ __device__ __forceinline__ float rms_scale(const float (&red)[4], int K, float e
   return 1.0f / sqrtf(total / (float)K + eps);
 }
 
+// D += A B on one 16x16x32 BF16 MFMA. Lane l holds A[l % 16][8 (l / 16) + e] and
+// B[8 (l / 16) + e][l % 16] (e = 0..7) and receives D[4 (l / 16) + r][l % 16] (r = 0..3).
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
 // Streaming 16-byte load: weights are read exactly once per call.
 __device__ __forceinline__ u32x4_t load_stream16(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
@@ -147,6 +154,13 @@ __device__ __forceinline__ uint32_t key_index(unsigned long long key) {
 
 __device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsigned long long b) {
   return a > b ? a : b;
+}
+
+// Largest key of the wave, in every lane.
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) k = key_max(k, __shfl_xor(k, off));
+  return k;
 }
 
 __device__ __forceinline__ float silu_f32(float g) {

@@ -54,6 +54,17 @@ struct StreamShape {
 bool stream_supported(int M, int rpw, int K, int kw, int epi);
 hipError_t launch_stream(const ProjArgs& a, int epi, const StreamShape& shape, hipStream_t stream);
 
+// Launch shape of the MFMA_STREAM kind (K = 32 S KW).
+struct MstreamShape {
+  int subtiles;  // T: 16-row MFMA subtiles per tile
+  int unroll;    // U: K steps of weight loads in flight per wave
+  int kw;        // waves per workgroup, splitting K (8 or 16)
+  int grid;      // workgroups; each walks <= mstream_max_depth(T, KW) tiles
+  int tiles;
+};
+bool mstream_supported(int M, int t, int K, int kw, int unroll, int epi, bool pro);
+hipError_t launch_mstream(const ProjArgs& a, int epi, const MstreamShape& shape, hipStream_t stream);
+
 // Launch shape of the MFMA kind.
 struct MfmaShape {
   int subtiles;  // T: 16-row MFMA subtiles per workgroup

@@ -26,11 +26,6 @@
 
 namespace ftk {
 
-__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                 0, 0, 0);
-}
-
 // rsqrt(mean(x[m]^2) + eps) per row: the arithmetic (per-thread order, wave
 // tree, fixed wave order) of the GEMV kind's prologue, so both kinds scale alike.
 __global__ __launch_bounds__(kThreads) void row_scale_kernel(const uint16_t* __restrict__ x, int K, float eps,

@@ -90,19 +90,18 @@ constexpr int kArgmaxBlock = 8192;
 
 int argmax_blocks(int vocab) { return (vocab + kArgmaxBlock - 1) / kArgmaxBlock; }
 
+// Largest key of a kThreads workgroup (valid in thread 0).
 __device__ __forceinline__ unsigned long long block_max_key(unsigned long long v, unsigned long long* red) {
-  red[threadIdx.x] = v;
+  v = wave_max_key(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = key_max(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
-  }
-  return red[0];
+  for (int w = 1; w < kWaves; ++w) v = key_max(v, red[w]);
+  return key_max(v, red[0]);
 }
 
 __global__ __launch_bounds__(kThreads) void argmax_block_kernel(const uint16_t* __restrict__ logits, int vocab,
                                                                 unsigned long long* __restrict__ keys, int rows) {
-  __shared__ unsigned long long red[kThreads];
+  __shared__ unsigned long long red[kWaves];
   const int row = blockIdx.y;
   const int begin = blockIdx.x * kArgmaxBlock;
   const int end = min(begin + kArgmaxBlock, vocab);
@@ -115,16 +114,33 @@ __global__ __launch_bounds__(kThreads) void argmax_block_kernel(const uint16_t* 
 }
 
 // Stage two: one workgroup per row picks the best of ``slots`` keys and writes
-// the id (and the winning logit) (argmax.py:34-48 _first_best).
-__global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
-                                                                   int slots, int rows, void* ids, int ids_bytes,
-                                                                   float* top) {
-  __shared__ unsigned long long red[kThreads];
+// the id (and the winning logit) (argmax.py:34-48 _first_best). The keys were
+// just written by other CUs, so every load is a long trip: each thread issues
+// its kFinalizeLoads loads together, and 1024 threads cover 8192 slots a round.
+constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizeLoads = 8;
+__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
+                                                                           int slots, int rows, void* ids,
+                                                                           int ids_bytes, float* top) {
+  __shared__ unsigned long long red[kFinalizeThreads / 64];
   const int row = blockIdx.x;
+  const int tid = threadIdx.x;
   unsigned long long best = 0ull;
-  for (int s = threadIdx.x; s < slots; s += kThreads) best = key_max(best, keys[(size_t)s * rows + row]);
-  best = block_max_key(best, red);
-  if (threadIdx.x == 0) {
+  for (int base = 0; base < slots; base += kFinalizeLoads * kFinalizeThreads) {
+    unsigned long long k[kFinalizeLoads];
+#pragma unroll
+    for (int u = 0; u < kFinalizeLoads; ++u) {
+      const int s = base + u * kFinalizeThreads + tid;
+      k[u] = s < slots ? keys[(size_t)s * rows + row] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < kFinalizeLoads; ++u) best = key_max(best, k[u]);
+  }
+  best = wave_max_key(best);
+  if ((tid & 63) == 0) red[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 0; w < kFinalizeThreads / 64; ++w) best = key_max(best, red[w]);
     const uint32_t idx = key_index(best);
     if (ids_bytes == 8)
       reinterpret_cast<int64_t*>(ids)[row] = (int64_t)idx;
@@ -177,8 +193,8 @@ hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids,
 
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(kThreads), 0, stream, keys, slots, M, ids, ids_bytes,
-                     top);
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(kFinalizeThreads), 0, stream, keys, slots, M, ids,
+                     ids_bytes, top);
   return hipGetLastError();
 }
 

@@ -33,8 +33,9 @@ FTK_HD int gemv_per_wave(int epi, int rpw) { return epi == EPI_SWIGLU ? rpw / 2 
 // Output columns: N (store / argmax) or I = N / 2 (SwiGLU pairs).
 FTK_HD int gemv_outputs(int epi, int n_rows) { return epi == EPI_SWIGLU ? n_rows / 2 : n_rows; }
 
-// Row groups per workgroup: the 4 waves in groups of KW waves that split K.
-FTK_HD int gemv_groups(int kw) { return kWaves / kw; }
+// Row groups per workgroup: the waves in groups of KW waves that split K (a
+// workgroup is 4 waves, or KW waves when KW > 4: one group).
+FTK_HD int gemv_groups(int kw) { return kw > kWaves ? 1 : kWaves / kw; }
 
 FTK_HD int gemv_tiles(int epi, int n_rows, int rpw, int kw) {
   const int per_tile = gemv_groups(kw) * gemv_per_wave(epi, rpw);
@@ -62,6 +63,13 @@ constexpr int kStreamMaxTiles = 8;  // tiles per workgroup: their wave totals wa
 // 16-byte chunks per lane per weight row (C), or 0 when K is not 512 C KW.
 FTK_HD int stream_chunks(int k, int kw) { return (kw < 1 || k % (512 * kw)) ? 0 : k / (512 * kw); }
 
+// Waves per STREAM workgroup: 4, or KW when one row group needs more (KW = 8).
+FTK_HD int stream_waves(int kw) { return kw > kWaves ? kw : kWaves; }
+
+// Largest M the STREAM kind takes: M <= 4 run exact-size kernels; 5..8 run the
+// 8-row kernel with the missing rows zero.
+constexpr int kStreamMaxRows = 8;
+
 // ---- M >= 4: BF16 MFMA skinny GEMM (T subtiles of 16 weight rows per workgroup)
 
 constexpr int kMfmaK = 32;          // K per MFMA step (v_mfma_f32_16x16x32_bf16)
@@ -86,6 +94,18 @@ FTK_HD int mfma_weight_row(int epi, int tile, int sub, int li, int n_rows, int t
   const int r = tile * 16 * t + sub * 16 + li;
   return r < n_rows ? r : n_rows - 1;
 }
+
+// ---- M = 5..16 with K = 32 S KW: the MFMA_STREAM kind -----------------------
+// A workgroup is KW waves that split K; a tile is 16 T weight rows (MFMA
+// subtiles, laid out as in the MFMA kind: mfma_weight_row / mfma_tiles). Wave
+// kw's step s covers k = 32 (kw S + s) .. + 31; lane l (li = l % 16, g = l / 16)
+// holds k = 32 (kw S + s) + 8 g .. + 7 of weight row li and of x row li.
+// Workgroup b walks tiles b, b + grid, ... (at most mstream_max_depth(T)).
+
+constexpr int kMstreamMaxRows = 16;
+FTK_HD int mstream_steps(int k, int kw) { return (kw < 1 || k % (32 * kw)) ? 0 : k / (32 * kw); }
+// Tiles a workgroup may walk: their per-wave partials wait in 64 KiB of LDS.
+FTK_HD int mstream_max_depth(int t, int kw) { return (64 * 1024) / (t * kw * 1024); }
 
 // ---- workspace layout of one projection call (bytes) -----------------------
 // Nothing in it carries state between calls: every slot a kernel reads was

@@ -25,20 +25,24 @@
 
 namespace ftk {
 
-template <int MR, int RPW, int C, int KW, bool PRO, int EPI>
-__global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles) {
-  constexpr int GROUPS = kWaves / KW;
+// MR: rows the kernel is built for; a.M <= MR rows are real (the rest are zero
+// and never stored). W: waves per workgroup (4, or 8 when KW = 8).
+template <int MR, int RPW, int C, int KW, int W, bool PRO, int EPI>
+__global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
+  constexpr int T = 64 * W;
+  constexpr int GROUPS = W / KW;
   constexpr int PW = (EPI == EPI_SWIGLU) ? RPW / 2 : RPW;  // outputs per row group per tile
   constexpr size_t kStep = (size_t)KW * 512;                // elements between a lane's chunks
-  __shared__ float part[kStreamMaxTiles][kWaves][RPW][MR];  // wave totals per tile
+  __shared__ float part[kStreamMaxTiles][W][RPW][MR];       // wave totals per tile
   __shared__ float red[MR][kWaves];
-  __shared__ unsigned long long best_lds[kWaves][MR];
+  __shared__ unsigned long long best_lds[W][MR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int grp = wave / KW, kw = wave - grp * KW;
   const int K = a.K;  // == 512 C KW (checked by the planner)
+  const int M = a.M;  // <= MR
   const int outputs = gemv_outputs(EPI, a.N);
   const size_t first = (size_t)(kw * 64 + lane) * 8;  // this lane's chunk j = 0
 
@@ -59,7 +63,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int j = 0; j < C; ++j) xr[m][j] = load16(a.x + (size_t)m * K + first + j * kStep);
+    for (int j = 0; j < C; ++j)
+      xr[m][j] = m < M ? load16(a.x + (size_t)m * K + first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
   u32x4_t g[PRO ? C : 1];
   if constexpr (PRO) {
 #pragma unroll
@@ -67,7 +72,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
   }
 
   // ---- first tile's weights in flight before the prologue -------------------
-  int tile = blockIdx.x;  // grid <= tiles
+  const int wg = blockIdx.x;  // tiles wg, wg + grid, ... (grid <= tiles)
+  int tile = wg;
   const uint16_t* wr[RPW];
   row_ptrs(tile, wr);
   u32x4_t wv[C][RPW];
@@ -79,21 +85,22 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
   // ---- RMSNorm prologue: normalise the slice in registers -------------------
   if constexpr (PRO) {
     // Sum of squares in the thread order of the other kinds' prologues
-    // (thread t: chunks t, t + 256, ...), so every kind scales a row alike.
-    // With KW = 4 thread t's own chunks (4 j + wave) 64 + lane are exactly
-    // those, in that order; otherwise re-read x in that order.
+    // (thread t < 256: chunks t, t + 256, ...), so every kind scales a row
+    // alike. With KW = W = 4 thread t's own chunks (4 j + wave) 64 + lane are
+    // exactly those, in that order; otherwise the first 4 waves re-read x.
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       float ss = 0.f;
-      if constexpr (KW == kWaves) {
+      if constexpr (KW == kWaves && W == kWaves) {
 #pragma unroll
         for (int j = 0; j < C; ++j) ss = sum_squares8(xr[m][j], ss);
       } else {
         const int KC = K >> 3;
-        for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(a.x + (size_t)m * K + (size_t)c * 8), ss);
+        if (m < M && tid < kThreads)
+          for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(a.x + (size_t)m * K + (size_t)c * 8), ss);
       }
       const float s = wave_sum(ss);
-      if (lane == 0) red[m][wave] = s;
+      if (lane == 0 && wave < kWaves) red[m][wave] = s;
     }
     __syncthreads();
 #pragma unroll
@@ -152,14 +159,15 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
 #pragma unroll
   for (int m = 0; m < MR; ++m) best[m] = 0ull;
   const int entries = count * GROUPS * PW;  // count is the same in every wave of the workgroup
-  for (int e = tid; e < entries; e += kThreads) {
+  for (int e = tid; e < entries; e += T) {
     const int p = e % PW;
     const int g = (e / PW) % GROUPS;
     const int i = e / (PW * GROUPS);
-    const int col = gemv_output(blockIdx.x + i * (int)gridDim.x, g, p, PW, GROUPS);
+    const int col = gemv_output(wg + i * (int)gridDim.x, g, p, PW, GROUPS);
     if (col >= outputs) continue;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
+      if (m >= M) break;
       float s = part[i][g * KW][p][m];
 #pragma unroll
       for (int k = 1; k < KW; ++k) s += part[i][g * KW + k][p][m];
@@ -182,15 +190,14 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
     // This workgroup's best key per input row; the finalize pass reduces the workgroups.
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) best[m] = key_max(best[m], __shfl_xor(best[m], off));
+      best[m] = wave_max_key(best[m]);
       if (lane == 0) best_lds[wave][m] = best[m];
     }
     __syncthreads();
-    if (tid < MR) {
+    if (tid < M) {
       unsigned long long k = best_lds[0][tid];
-      for (int w = 1; w < kWaves; ++w) k = key_max(k, best_lds[w][tid]);
-      a.keys[(size_t)blockIdx.x * MR + tid] = k;
+      for (int w = 1; w < W; ++w) k = key_max(k, best_lds[w][tid]);
+      a.keys[(size_t)blockIdx.x * M + tid] = k;
     }
   }
 }
@@ -200,7 +207,8 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(ProjArgs a, int tiles)
 typedef void (*StreamKernel)(ProjArgs, int);
 
 // Instantiated (rows per group, C, KW): the K of each model shape of the path
-// (1024, 2048, 3072, 4096, 12288) with two or three row-group sizes each.
+// (1024, 2048, 3072, 4096, 12288) with two or three row-group sizes each; the
+// 8-row kernel (M = 5..8) for the 8B model's K (4096, 12288).
 #define FTK_STREAM_SHAPES(MR, PRO, EPI)   \
   FTK_STREAM_SHAPE(MR, 2, 1, 2, PRO, EPI) \
   FTK_STREAM_SHAPE(MR, 4, 1, 2, PRO, EPI) \
@@ -213,14 +221,25 @@ typedef void (*StreamKernel)(ProjArgs, int);
   FTK_STREAM_SHAPE(MR, 4, 2, 4, PRO, EPI) \
   FTK_STREAM_SHAPE(MR, 8, 2, 4, PRO, EPI) \
   FTK_STREAM_SHAPE(MR, 2, 6, 4, PRO, EPI) \
-  FTK_STREAM_SHAPE(MR, 4, 6, 4, PRO, EPI)
+  FTK_STREAM_SHAPE(MR, 4, 6, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(MR, 2, 3, 8, PRO, EPI)
+
+#define FTK_STREAM_SHAPES_8(PRO, EPI)    \
+  FTK_STREAM_SHAPE(8, 2, 2, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(8, 4, 2, 4, PRO, EPI) \
+  FTK_STREAM_SHAPE(8, 2, 3, 8, PRO, EPI) \
+  FTK_STREAM_SHAPE(8, 4, 3, 8, PRO, EPI)
 
 #define FTK_STREAM_SHAPE(MR, R, CC, KW, PRO, EPI) \
-  if (rpw == R && c == CC && kw == KW) return stream_kernel<MR, R, CC, KW, PRO, EPI>;
+  if (rpw == R && c == CC && kw == KW) return stream_kernel<MR, R, CC, KW, (KW > kWaves ? KW : kWaves), PRO, EPI>;
 
 template <int MR, bool PRO, int EPI>
 static StreamKernel pick_stream_shape(int rpw, int c, int kw) {
-  FTK_STREAM_SHAPES(MR, PRO, EPI)
+  if constexpr (MR == kStreamMaxRows) {
+    FTK_STREAM_SHAPES_8(PRO, EPI)
+  } else {
+    FTK_STREAM_SHAPES(MR, PRO, EPI)
+  }
   return nullptr;
 }
 #undef FTK_STREAM_SHAPE
@@ -244,6 +263,10 @@ static StreamKernel pick_stream(int M, int rpw, int c, int kw, bool pro, int epi
     case 2: return pick_stream_mr<2>(rpw, c, kw, pro, epi);
     case 3: return pick_stream_mr<3>(rpw, c, kw, pro, epi);
     case 4: return pick_stream_mr<4>(rpw, c, kw, pro, epi);
+    case 5:
+    case 6:
+    case 7:
+    case 8: return pick_stream_mr<kStreamMaxRows>(rpw, c, kw, pro, epi);
   }
   return nullptr;
 }
@@ -260,7 +283,7 @@ hipError_t launch_stream(const ProjArgs& a, int epi, const StreamShape& s, hipSt
   // Every workgroup walks at most kStreamMaxTiles tiles (their totals wait in LDS).
   if (s.grid < 1 || s.grid > s.tiles || (s.tiles + s.grid - 1) / s.grid > kStreamMaxTiles)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k, dim3(s.grid), dim3(kThreads), 0, stream, a, s.tiles);
+  hipLaunchKernelGGL(k, dim3(s.grid), dim3(64 * stream_waves(s.kw)), 0, stream, a, s.tiles);
   return hipGetLastError();
 }
 

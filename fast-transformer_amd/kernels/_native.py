@@ -16,7 +16,8 @@ LIB_PATH = Path(__file__).with_name("libftk.so")
 
 FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = range(5)
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
-KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM = range(5)
+PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
+KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM = range(6)
 MAX_ROWS = 32
 
 _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -162,6 +163,7 @@ def argmax_workspace(device, rows, vocab):
     return workspace(device, int(lib().ftk_argmax_workspace_bytes(rows, vocab)), "argmax")
 
 
-def project_workspace(device, m, n, k, epilogue, config=None):
-    """Workspace of one projection call (split-K partials, row scales, argmax keys)."""
-    return workspace(device, int(lib().ftk_project_workspace_bytes(m, n, k, epilogue, config)), "project")
+def project_workspace(device, m, n, k, epilogue, config=None, prologue=False):
+    """Workspace of one projection call (row scales, argmax keys); ``prologue``: the call has gamma."""
+    flags = epilogue | (PLAN_PROLOGUE if prologue else 0)
+    return workspace(device, int(lib().ftk_project_workspace_bytes(m, n, k, flags, config)), "project")

@@ -53,7 +53,7 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     v = weight.shape[0]
     ids = torch.empty(shape[:-1], dtype=ids_dtype, device=x.device)
     out = torch.empty((*shape[:-1], v), dtype=torch.bfloat16, device=x.device) if logits else None
-    ws = _native.project_workspace(x.device, m, v, k, _native.EPI_ARGMAX, config)
+    ws = _native.project_workspace(x.device, m, v, k, _native.EPI_ARGMAX, config, prologue=norm_weight is not None)
     ids_bytes = {torch.int64: 8, torch.int32: 4}[ids_dtype]
     status = _native.try_call(
         "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),

@@ -86,7 +86,7 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
     m, k = flat.shape
     n = weight.shape[0]
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
-    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config)
+    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config, prologue=True)
     status = _native.try_call(
         "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
         _native.ptr(out), m, n, k, _native.EPI_STORE, None, 0, None, _native.ptr(ws), ws.numel(), config,
@@ -183,8 +183,9 @@ def linear(x, weight, split_ok=False):
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
 
-def plan(m, n, k, epilogue=_native.EPI_STORE, compute_units=256, config=None):
+def plan(m, n, k, epilogue=_native.EPI_STORE, compute_units=256, config=None, prologue=False):
     """The launch the C planner makes for a shape (host only; no device needed)."""
     p = _native.Plan()
-    _native.call("ftk_plan_project", m, n, k, epilogue, compute_units, config, p)
+    flags = epilogue | (_native.PLAN_PROLOGUE if prologue else 0)
+    _native.call("ftk_plan_project", m, n, k, flags, compute_units, config, p)
     return p

@@ -39,7 +39,7 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None):
     if n % 2:
         raise ValueError("gate_up_weight must stack gate and up rows: an even row count")
     out = torch.empty((m, n // 2), device=x.device, dtype=torch.bfloat16)
-    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_SWIGLU, config)
+    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_SWIGLU, config, prologue=norm_weight is not None)
     status = _native.try_call(
         "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(gate_up_weight),
         _native.ptr(out), m, n, k, _native.EPI_SWIGLU, None, 0, None, _native.ptr(ws), ws.numel(), config,

@@ -50,13 +50,19 @@ typedef enum ftk_epilogue {
   FTK_EPI_ARGMAX = 2   /* logits (optional) + lowest-index greedy id per row */
 } ftk_epilogue;
 
+/* OR-ed into the epilogue argument of ftk_plan_project / ftk_project_workspace_bytes:
+ * plan a call that has the RMSNorm prologue (gamma != NULL). Some launch shapes
+ * exist only without it, so the plan (and the workspace size) can differ. */
+#define FTK_PLAN_PROLOGUE 0x100
+
 typedef enum ftk_kind {
   FTK_KIND_AUTO = 0,
   FTK_KIND_GEMV = 1,     /* M <= 4: HBM-streaming GEMV (v_dot2_f32_bf16, LDS-resident x) */
   FTK_KIND_MFMA = 2,     /* M >= 4: v_mfma_f32_16x16x32_bf16 tiles */
   FTK_KIND_GENERIC = 3,  /* any shape/alignment, scalar loads; store epilogue only */
-  FTK_KIND_STREAM = 4    /* M <= 4, K = 512 C KW: HBM-streaming GEMV, x slice in registers,
+  FTK_KIND_STREAM = 4,   /* M <= 8, K = 512 C KW: HBM-streaming GEMV, x slice in registers,
                             rolling weight prefetch, one barrier per workgroup */
+  FTK_KIND_MFMA_STREAM = 5  /* M <= 16, K = 32 S KW: the STREAM schedule on 16x16x32 MFMA tiles */
 } ftk_kind;
 
 /* Launch choice for one projection (the reference's per-shape config tuple,
@@ -65,14 +71,17 @@ typedef enum ftk_kind {
 typedef struct ftk_config {
   int kind;            /* ftk_kind */
   int rows_per_wave;   /* GEMV, STREAM: weight rows per row group per tile (1..8);
-                          MFMA: rows per workgroup (16, 32, 64) */
+                          MFMA: rows per workgroup (16, 32, 64); MFMA_STREAM: rows per tile (16, 32) */
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
                           MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4);
-                          STREAM: unused (K fixes the chunks per lane) */
-  int groups_per_cu;   /* GEMV, STREAM: grid cap = groups_per_cu * CUs (grid-stride beyond; STREAM
-                          raises the grid so no workgroup walks more than 8 tiles); MFMA: unused */
-  int waves;           /* MFMA: waves per workgroup splitting K (4, 8, 16);
-                          GEMV, STREAM: waves per row group splitting K (1, 2, 4; a workgroup is 4 waves) */
+                          STREAM: unused (K fixes the chunks per lane);
+                          MFMA_STREAM: K steps of weight loads in flight per wave (2, 4, 8) */
+  int groups_per_cu;   /* GEMV, STREAM, MFMA_STREAM: grid cap = groups_per_cu * CUs (grid-stride
+                          beyond; the STREAM kinds raise the grid so no workgroup walks more tiles
+                          than its LDS holds); MFMA: unused */
+  int waves;           /* MFMA, MFMA_STREAM: waves per workgroup splitting K (4, 8, 16);
+                          GEMV, STREAM: waves per row group splitting K (1, 2, 4, 8; a workgroup is
+                          4 waves, or 8 when 8 split K) */
 } ftk_config;
 
 typedef struct ftk_plan {
@@ -127,7 +136,8 @@ int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const v
 
 /* Workspace bytes ftk_project_bf16 needs for this shape on the current device:
  * per-workgroup argmax keys (FTK_EPI_ARGMAX) and the RMSNorm row scales of the
- * MFMA kind (gamma != NULL, M > 4). Other calls need none (NULL is fine). */
+ * MFMA kind (gamma != NULL). Other calls need none (NULL is fine). OR
+ * FTK_PLAN_PROLOGUE into `epilogue` for a call with gamma. */
 int64_t ftk_project_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue, const ftk_config* cfg);
 
 /* General form of the three above with an explicit launch choice (cfg may be
@@ -167,7 +177,8 @@ int64_t ftk_argmax_workspace_bytes(int64_t rows, int64_t vocab);
 
 /* ---- planning (host only, no device needed) ---------------------------------- */
 
-/* The launch ftk_project_bf16 would make for this shape on `compute_units` CUs. */
+/* The launch ftk_project_bf16 would make for this shape on `compute_units` CUs
+ * (`epilogue` | FTK_PLAN_PROLOGUE for a call with gamma). */
 int ftk_plan_project(int64_t M, int64_t N, int64_t K, int epilogue, int compute_units, const ftk_config* cfg,
                      ftk_plan* plan);
 

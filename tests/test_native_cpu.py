@@ -85,26 +85,47 @@ def _coverage(plan, n, epilogue):
     return np.frombuffer(counts, dtype=np.int32), max_row.value
 
 
-#: (rows per group, chunks per lane C, KW) the STREAM kind instantiates (K = 512 C KW).
+#: (rows per group, chunks per lane C, KW) the STREAM kind instantiates (K = 512 C KW), for
+#: M <= 4 and for the 8-row kernel (M = 5..8).
 STREAM_SHAPES = ((2, 1, 2), (4, 1, 2), (8, 1, 2), (2, 1, 4), (4, 1, 4), (2, 3, 2), (4, 3, 2), (2, 2, 4), (4, 2, 4),
-                 (8, 2, 4), (2, 6, 4), (4, 6, 4))
+                 (8, 2, 4), (2, 6, 4), (4, 6, 4), (2, 3, 8))
+STREAM_SHAPES_8 = ((2, 2, 4), (4, 2, 4), (2, 3, 8), (4, 3, 8))
 
 
-def _stream_status(k, rpw, kw):
-    if k % (512 * kw):
+def _stream_status(m, k, rpw, kw):
+    if m > 8 or k % (512 * kw):
         return _native.FTK_ERR_UNSUPPORTED
-    return _native.FTK_OK if (rpw, k // (512 * kw), kw) in STREAM_SHAPES else _native.FTK_ERR_INVALID
+    shapes = STREAM_SHAPES if m <= 4 else STREAM_SHAPES_8
+    return _native.FTK_OK if (rpw, k // (512 * kw), kw) in shapes else _native.FTK_ERR_INVALID
+
+
+#: (T, S, KW, U) the MFMA_STREAM kind instantiates (K = 32 S KW), by epilogue, without the prologue.
+MSTREAM_EVEN = ((2, 8, 16, 4), (2, 16, 8, 4), (2, 16, 8, 8), (2, 16, 8, 16), (2, 8, 16, 8))
+MSTREAM_ONE = ((1, 8, 16, 4), (1, 8, 16, 8), (1, 16, 8, 4), (1, 16, 8, 8), (1, 16, 8, 16), (1, 24, 16, 2))
+
+
+def _mstream_shapes(epilogue):
+    return MSTREAM_EVEN + (() if epilogue == _native.EPI_SWIGLU else MSTREAM_ONE)
+
+
+def _mstream_status(m, k, epilogue, t, kw, u):
+    if m > 16 or k % (32 * kw):
+        return _native.FTK_ERR_UNSUPPORTED
+    return _native.FTK_OK if (t, k // (32 * kw), kw, u) in _mstream_shapes(epilogue) else _native.FTK_ERR_INVALID
 
 
 def _configs(m):
+    gemv = []
     if m <= 4:
         gemv = [_native.Config(_native.KIND_GEMV, rpw, u, gpc, kw)
                 for rpw, u, kw in ((2, 4, 1), (4, 2, 1), (8, 1, 1), (1, 2, 2), (2, 2, 2), (1, 1, 4), (2, 2, 4))
                 for gpc in (1, 8)]
+    if m <= 8:
         gemv += [_native.Config(_native.KIND_STREAM, rpw, 0, gpc, kw)
-                 for rpw, _, kw in STREAM_SHAPES for gpc in (1, 8, 16)]
-    else:
-        gemv = []
+                 for rpw, _, kw in (STREAM_SHAPES if m <= 4 else STREAM_SHAPES_8) for gpc in (1, 8, 16)]
+    if m <= 16:
+        gemv += [_native.Config(_native.KIND_MFMA_STREAM, 16 * t, u, gpc, kw)
+                 for t, _, kw, u in MSTREAM_EVEN + MSTREAM_ONE for gpc in (1, 4)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
             for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
     return [None] + gemv + mfma
@@ -128,7 +149,12 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert status == _native.FTK_ERR_UNSUPPORTED
                 continue
             if cfg is not None and cfg.kind == _native.KIND_STREAM:
-                want = _stream_status(k, cfg.rows_per_wave, cfg.waves)
+                want = _stream_status(m, k, cfg.rows_per_wave, cfg.waves)
+                assert status == want, (m, n, k, epilogue, cfg)
+                if want != _native.FTK_OK:
+                    continue
+            if cfg is not None and cfg.kind == _native.KIND_MFMA_STREAM:
+                want = _mstream_status(m, k, epilogue, cfg.rows_per_wave // 16, cfg.waves, cfg.unroll)
                 assert status == want, (m, n, k, epilogue, cfg)
                 if want != _native.FTK_OK:
                     continue
@@ -143,6 +169,11 @@ def test_plan_writes_every_output_once(m, n, k):
                 # every walk equally deep (within one tile) and at most 8 tiles: their totals wait in LDS
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
                 assert p.unroll * 512 * p.waves == k and p.lds_bytes == 0
+                assert p.threads == 64 * max(4, p.waves)
+            if p.kind == _native.KIND_MFMA_STREAM:
+                t = p.rows_per_wave // 16
+                assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
+                assert p.threads == 64 * p.waves and k % (32 * p.waves) == 0
             if p.kind == _native.KIND_MFMA:
                 # one workgroup per tile over all of K: no split-K, nothing shared between workgroups
                 assert p.grid == p.tiles and p.splits == 1 and p.k_slice == k
@@ -160,7 +191,20 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
-    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # MFMA tiles on the STREAM schedule
+    assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 512 and p.unroll == 8
+    _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # small, with the norm
+    assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 1024 and p.unroll == 4
+    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K at M <= 8: the 8-row STREAM kernel
+    assert p.kind == _native.KIND_STREAM and p.waves == 8
+    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
+    assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 16 and p.unroll == 2
+    # K = 12288 with the prologue has no MFMA_STREAM kernel: the 8-row STREAM kernel (8 waves split K)
+    _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
+    _native.call("ftk_plan_project", 5, 4096, 2048, 0, 256, None, p)  # neither STREAM kind has this K
     assert p.kind == _native.KIND_MFMA and p.grid == 256 and p.splits == 1
-    _native.call("ftk_plan_project", 16, 24576, 4096, _native.EPI_SWIGLU, 256, None, p)
+    _native.call("ftk_plan_project", 17, 4096, 4096, 0, 256, None, p)
+    assert p.kind == _native.KIND_MFMA
+    _native.call("ftk_plan_project", 20, 24576, 4096, _native.EPI_SWIGLU, 256, None, p)
     assert p.kind == _native.KIND_MFMA and p.rows_per_wave == 32 and p.grid == 12288 // 16
