@@ -98,6 +98,7 @@ class Step:
         self.h = torch.randn((m, cfg["hidden"]), generator=g, device=device).to(torch.bfloat16)
         # attention output feeding O: attention itself is outside the path
         self.attn = torch.randn((m, model.q), generator=g, device=device).to(torch.bfloat16)
+        self.resid = torch.randn((m, cfg["hidden"]), generator=g, device=device).to(torch.bfloat16)
         self.top = torch.empty(m, dtype=torch.float32, device=device)
 
     def layer(self, lw, h):
@@ -111,6 +112,17 @@ class Step:
         for lw in self.model.layers:
             _, h = self.layer(lw, h)
         return h
+
+    def layers_residual(self):
+        """The same projections in the decode data flow of engine/decode.py:229-261: each input
+        norm also adds the residual stream and stores the new one (add_rms_norm folded in)."""
+        hidden, resid = self.h, self.resid
+        for lw in self.model.layers:
+            _, resid = L.add_rms_norm_linear(hidden, resid, lw["ln1"], EPS, lw["qkv"])
+            o = L.linear(self.attn, lw["o"])
+            act, resid = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS, residual=resid)
+            hidden = L.linear(act, lw["down"])
+        return hidden, resid
 
     def run(self):
         h = self.layers()
@@ -356,6 +368,10 @@ def shapes_table(model8, step8, dev):
     g = capture(step8.layers)
     us = time_graph(g, reps=5) / cfg["layers"]
     out["C3 8B layer M=1"] = shape_entry(us, sum(lb.values()))
+    # ... and in the decode data flow: both norms also add the residual and store the new stream
+    g = capture(step8.layers_residual)
+    us = time_graph(g, reps=5) / cfg["layers"]
+    out["C3 8B layer M=1, residual-add prologues"] = shape_entry(us, sum(lb.values()) + 4 * 2 * cfg["hidden"])
     # C1 / C2: Qwen3-0.6B shapes
     model06 = Model(QWEN3_06B, dev, head=False, seed=2)
     st06 = Step(model06, 1, dev, seed=3)

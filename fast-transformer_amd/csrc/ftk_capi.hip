@@ -373,14 +373,35 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
   return FTK_OK;
 }
 
-int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M, int64_t N,
-                     int64_t K, int epilogue, void* ids, int ids_bytes, float* top, void* workspace,
-                     int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
+static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+  if (a == nullptr || b == nullptr) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + (uintptr_t)b_bytes && pb < pa + (uintptr_t)a_bytes;
+}
+
+int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma, float eps, const void* w, void* y,
+                          int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
+                          void* workspace, int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
   if (x == nullptr || w == nullptr) return FTK_ERR_INVALID;
   if (epilogue != FTK_EPI_ARGMAX && y == nullptr) return FTK_ERR_INVALID;
   if (epilogue == FTK_EPI_ARGMAX) {
     if (ids == nullptr || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
     if (workspace == nullptr) return FTK_ERR_WORKSPACE;
+  }
+  ftk_rows r = {nullptr, nullptr, nullptr, 0};
+  if (rows != nullptr) r = *rows;
+  const bool extra = r.residual != nullptr || r.sum != nullptr || r.x_ids != nullptr;
+  if (extra) {
+    if (gamma == nullptr) return FTK_ERR_INVALID;  // the rows feed the norm
+    if (r.x_ids != nullptr && r.x_ids_bytes != 4 && r.x_ids_bytes != 8) return FTK_ERR_INVALID;
+    if (M < 1 || K < 1 || M > FTK_MAX_ROWS || K > INT32_MAX) return FTK_ERR_INVALID;
+    // Workgroup 0 writes sum while every workgroup reads x and the residual.
+    const int64_t rows_bytes = M * K * 2;
+    const int64_t out_cols = epilogue == FTK_EPI_SWIGLU ? N / 2 : N;
+    if ((r.x_ids == nullptr && overlaps(r.sum, rows_bytes, x, rows_bytes)) ||
+        overlaps(r.sum, rows_bytes, r.residual, rows_bytes) || overlaps(r.sum, rows_bytes, y, M * out_cols * 2))
+      return FTK_ERR_INVALID;
+    if ((r.residual && !aligned16(r.residual)) || (r.sum && !aligned16(r.sum))) return FTK_ERR_UNSUPPORTED;
   }
   DeviceInfo d = device_info();
   if (!d.ok) return hip_status(hipErrorNoDevice);
@@ -409,6 +430,13 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   a.ids = ids;
   a.ids_bytes = ids_bytes;
   a.top = top;
+  a.residual = (const uint16_t*)r.residual;
+  a.sum = (uint16_t*)r.sum;
+  a.x_ids = r.x_ids;
+  a.x_ids_bytes = r.x_ids_bytes;
+  // The MFMA kind's projection reads the pre-pass's stored rows: it needs sum.
+  if (p.kind == FTK_KIND_MFMA && (r.residual != nullptr || r.x_ids != nullptr) && r.sum == nullptr)
+    return FTK_ERR_UNSUPPORTED;
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   hipError_t e;
@@ -430,6 +458,13 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
   if (e == hipSuccess && epilogue == FTK_EPI_ARGMAX)
     e = launch_argmax_finalize(a.keys, p.grid, (int)M, ids, ids_bytes, top, s);
   return hip_status(e);
+}
+
+int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M, int64_t N,
+                     int64_t K, int epilogue, void* ids, int ids_bytes, float* top, void* workspace,
+                     int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
+  return ftk_project_rows_bf16(x, nullptr, gamma, eps, w, y, M, N, K, epilogue, ids, ids_bytes, top, workspace,
+                               workspace_bytes, cfg, stream);
 }
 
 int ftk_linear_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
@@ -488,6 +523,16 @@ int ftk_add_rms_norm_bf16(const void* x, int x_splits, int64_t x_split_stride, c
   return hip_status(launch_add_rms_norm(x, x_splits, x_split_stride, (const uint16_t*)residual,
                                         (const uint16_t*)gamma, (uint16_t*)y, (uint16_t*)sum, (int)rows, (int)cols,
                                         eps, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int ftk_embed_rms_norm_bf16(const void* ids, int ids_bytes, const void* table, const void* gamma, void* y,
+                            void* hidden, int64_t rows, int64_t cols, float eps, void* stream) {
+  if (!ids || !table || !gamma || !y || !hidden || (ids_bytes != 4 && ids_bytes != 8) || rows < 1 || cols < 1 ||
+      rows > INT32_MAX || cols > INT32_MAX)
+    return FTK_ERR_INVALID;
+  return hip_status(launch_embed_rms_norm(ids, ids_bytes, (const uint16_t*)table, (const uint16_t*)gamma,
+                                          (uint16_t*)y, (uint16_t*)hidden, (int)rows, (int)cols, eps,
+                                          reinterpret_cast<hipStream_t>(stream)));
 }
 
 int ftk_swiglu_bf16(const void* packed, int splits, int64_t split_stride, void* out, int64_t rows, int64_t width,

@@ -84,6 +84,19 @@ __device__ __forceinline__ u32x4_t norm8(u32x4_t v, u32x4_t g, float scale) {
   return u32x4_t{o[0], o[1], o[2], o[3]};
 }
 
+// The residual add of the prologue: bf16(f32(x) + f32(r)) for 8 BF16 values
+// (engine/kernels/rmsnorm.py:86-88, a BF16 tensor addition).
+__device__ __forceinline__ u32x4_t add8(u32x4_t x, u32x4_t r) {
+  const uint32_t e[4] = {x[0], x[1], x[2], x[3]};
+  const uint32_t f[4] = {r[0], r[1], r[2], r[3]};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = pack_bf16(lo_f32(e[i]) + lo_f32(f[i]), hi_f32(e[i]) + hi_f32(f[i]));
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ void store16(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+
 // rsqrt(mean + eps) from the four wave totals of a workgroup, summed in wave order.
 __device__ __forceinline__ float rms_scale(const float (&red)[4], int K, float eps) {
   const float total = ((red[0] + red[1]) + red[2]) + red[3];

@@ -86,13 +86,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
     for (int c = tid; c < KC; c += kThreads) gs[c] = load16(a.gamma + (size_t)c * 8);
   }
   float ss[MR];
+  const bool keep = PRO && a.sum != nullptr && blockIdx.x == 0;  // workgroup 0 stores x + residual
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     ss[m] = 0.f;
+    const uint16_t* xr = PRO ? x_row(a, m) : a.x + (size_t)m * K;
     for (int c = tid; c < KC; c += kThreads) {
-      const u32x4_t v = load16(a.x + (size_t)m * K + (size_t)c * 8);
+      const u32x4_t v = PRO ? prologue_in(a, xr, m, (size_t)c * 8) : load16(xr + (size_t)c * 8);
       xs[m * KC + c] = v;
-      if constexpr (PRO) ss[m] = sum_squares8(v, ss[m]);
+      if constexpr (PRO) {
+        ss[m] = sum_squares8(v, ss[m]);
+        if (keep) store16(a.sum + (size_t)m * K + (size_t)c * 8, v);
+      }
     }
   }
   if constexpr (PRO) {

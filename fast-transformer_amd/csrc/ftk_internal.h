@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ftk_device.h"
 #include "ftk_plan.h"
 
 namespace ftk {
@@ -21,7 +22,30 @@ struct ProjArgs {
   int ids_bytes;
   float* top;             // [M] winning logit as FP32, or null
   unsigned long long* keys;  // [grid][M] per-workgroup best keys (workspace)
+  // Prologue inputs beyond x (gamma != null only): the rows the norm reads are
+  //   s[m] = bf16(xrow(m) + residual[m])   (or xrow(m) without a residual),
+  // xrow(m) = x[x_ids[m]] (an embedding gather) or x[m]. Workgroup 0 stores s
+  // into sum when sum != null.
+  const uint16_t* residual;  // [M, K] or null
+  uint16_t* sum;             // [M, K] or null
+  const void* x_ids;         // [M] int32 / int64 row indices into x, or null
+  int x_ids_bytes;
 };
+
+// Row m of the prologue's x: x[x_ids[m]] (embedding gather) or x[m].
+__device__ __forceinline__ const uint16_t* x_row(const ProjArgs& a, int m) {
+  if (a.x_ids == nullptr) return a.x + (size_t)m * a.K;
+  const int64_t id = a.x_ids_bytes == 8 ? reinterpret_cast<const int64_t*>(a.x_ids)[m]
+                                        : (int64_t) reinterpret_cast<const int32_t*>(a.x_ids)[m];
+  return a.x + (size_t)id * a.K;
+}
+
+// 8 BF16 values of the prologue's input row m at element k: x (+ residual).
+__device__ __forceinline__ u32x4_t prologue_in(const ProjArgs& a, const uint16_t* xr, int m, size_t k) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + k);
+  if (a.residual == nullptr) return v;
+  return add8(v, *reinterpret_cast<const u32x4_t*>(a.residual + (size_t)m * a.K + k));
+}
 
 // Launch shape of the GEMV kind.
 struct GemvShape {
@@ -89,6 +113,8 @@ hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y
 // Standalone operators (the reference's separate kernels).
 hipError_t launch_rms_norm(const uint16_t* x, int64_t row_stride, const uint16_t* gamma, uint16_t* y, int rows,
                            int cols, float eps, hipStream_t stream);
+hipError_t launch_embed_rms_norm(const void* ids, int ids_bytes, const uint16_t* table, const uint16_t* gamma,
+                                 uint16_t* y, uint16_t* hidden, int rows, int cols, float eps, hipStream_t stream);
 hipError_t launch_add_rms_norm(const void* x, int splits, int64_t split_stride, const uint16_t* residual,
                                const uint16_t* gamma, uint16_t* y, uint16_t* sum, int rows, int cols, float eps,
                                hipStream_t stream);

@@ -28,18 +28,23 @@ namespace ftk {
 
 // rsqrt(mean(x[m]^2) + eps) per row: the arithmetic (per-thread order, wave
 // tree, fixed wave order) of the GEMV kind's prologue, so both kinds scale alike.
-__global__ __launch_bounds__(kThreads) void row_scale_kernel(const uint16_t* __restrict__ x, int K, float eps,
-                                                             float* __restrict__ scale) {
+// With a residual or gathered rows it also stores the rows it normalises
+// (x + residual) into a.sum, which the projection kernel then reads as its x.
+__global__ __launch_bounds__(kThreads) void row_scale_kernel(ProjArgs a, float* __restrict__ scale) {
   __shared__ float red[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int KC = K >> 3;
-  const uint16_t* xr = x + (size_t)blockIdx.x * K;
+  const int m = blockIdx.x, K = a.K, KC = K >> 3;
+  const uint16_t* xr = x_row(a, m);
   float ss = 0.f;
-  for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(xr + (size_t)c * 8), ss);
+  for (int c = tid; c < KC; c += kThreads) {
+    const u32x4_t v = prologue_in(a, xr, m, (size_t)c * 8);
+    ss = sum_squares8(v, ss);
+    if (a.sum != nullptr) store16(a.sum + (size_t)m * K + (size_t)c * 8, v);
+  }
   const float s = wave_sum(ss);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (tid == 0) scale[blockIdx.x] = rms_scale(red, K, eps);
+  if (tid == 0) scale[m] = rms_scale(red, K, a.eps);
 }
 
 template <int MB, int T, int U, int W, int EPI, bool PRO>
@@ -251,13 +256,21 @@ bool mfma_supported(int M, int t, int unroll, int waves, int epi) {
 hipError_t launch_mfma(const ProjArgs& a, int epi, const MfmaShape& s, const MfmaArgs& p, hipStream_t stream) {
   MfmaKernel k = pick_mfma(a.M, s.subtiles, s.unroll, s.waves, epi, a.gamma != nullptr);
   if (k == nullptr) return hipErrorInvalidValue;
+  ProjArgs main = a;
   if (a.gamma != nullptr) {
-    hipLaunchKernelGGL(row_scale_kernel, dim3(a.M), dim3(kThreads), 0, stream, a.x, a.K, a.eps,
-                       const_cast<float*>(p.row_scale));
+    hipLaunchKernelGGL(row_scale_kernel, dim3(a.M), dim3(kThreads), 0, stream, a, const_cast<float*>(p.row_scale));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (a.residual != nullptr || a.x_ids != nullptr) {
+      // the projection reads the rows the pre-pass stored (x + residual, or the gathered rows)
+      if (a.sum == nullptr) return hipErrorInvalidValue;
+      main.x = a.sum;
+      main.residual = nullptr;
+      main.x_ids = nullptr;
+    }
+    main.sum = nullptr;
   }
-  hipLaunchKernelGGL(k, dim3(s.grid), dim3(64 * s.waves), 0, stream, a, p);
+  hipLaunchKernelGGL(k, dim3(s.grid), dim3(64 * s.waves), 0, stream, main, p);
   return hipGetLastError();
 }
 

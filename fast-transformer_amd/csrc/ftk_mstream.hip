@@ -44,9 +44,12 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
   auto koff = [&](int s) { return (size_t)(32 * (kw * S + s) + 8 * g); };
 
   // ---- x slice first, then the first weight window ----------------------------
+  // With the prologue, row li is x[li] or the gathered x[x_ids[li]], plus the residual.
+  const uint16_t* xrow = (PRO && mine) ? x_row(a, li) : a.x + (size_t)li * K;
   u32x4_t xr[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) xr[s] = mine ? load16(a.x + (size_t)li * K + koff(s)) : u32x4_t{0u, 0u, 0u, 0u};
+  for (int s = 0; s < S; ++s)
+    xr[s] = !mine ? u32x4_t{0u, 0u, 0u, 0u} : PRO ? prologue_in(a, xrow, li, koff(s)) : load16(xrow + koff(s));
 
   const int wg = blockIdx.x;
   int tile = wg;  // grid <= tiles
@@ -70,6 +73,11 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
     ss += __shfl_xor(ss, 16);  // the four lane groups holding row li, pairwise:
     ss += __shfl_xor(ss, 32);  // (g0 + g1) + (g2 + g3) in every one of them
     if (g == 0) red[kw][li] = ss;
+    // The normalised rows themselves (x + residual) go out once, from workgroup 0.
+    if (a.sum != nullptr && blockIdx.x == 0 && mine) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) store16(a.sum + (size_t)li * K + koff(s), xr[s]);
+    }
     __syncthreads();
     float total = red[0][li];
 #pragma unroll

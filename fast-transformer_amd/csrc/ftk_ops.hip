@@ -49,6 +49,34 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const uint16_t* __re
   }
 }
 
+// embed_rms_norm (engine/kernels/rmsnorm.py:128-162): row r is table[ids[r]],
+// copied out as the residual stream and normalised like rms_norm.
+__global__ __launch_bounds__(kThreads) void embed_rms_norm_kernel(const void* __restrict__ ids, int ids_bytes,
+                                                                  const uint16_t* __restrict__ table,
+                                                                  const uint16_t* __restrict__ gamma,
+                                                                  uint16_t* __restrict__ y,
+                                                                  uint16_t* __restrict__ hidden, int cols, float eps) {
+  __shared__ float red[kWaves];
+  const int r = blockIdx.x;
+  const int64_t id = ids_bytes == 8 ? reinterpret_cast<const int64_t*>(ids)[r]
+                                    : (int64_t) reinterpret_cast<const int32_t*>(ids)[r];
+  const uint16_t* xr = table + id * cols;
+  uint16_t* hr = hidden + (int64_t)r * cols;
+  uint16_t* yr = y + (int64_t)r * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const uint16_t v = xr[c];
+    hr[c] = v;
+    const float f = bf16_to_f32(v);
+    ss += f * f;
+  }
+  const float scale = 1.0f / sqrtf(block_sum(ss, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float n = round_bf16(bf16_to_f32(xr[c]) * scale);
+    yr[c] = (uint16_t)f32_to_bf16(n * bf16_to_f32(gamma[c]));
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void add_rms_norm_kernel(const void* __restrict__ x, int splits,
                                                                 int64_t split_stride,
                                                                 const uint16_t* __restrict__ residual,
@@ -162,6 +190,13 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const float* __r
 hipError_t launch_rms_norm(const uint16_t* x, int64_t row_stride, const uint16_t* gamma, uint16_t* y, int rows,
                            int cols, float eps, hipStream_t stream) {
   hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, row_stride, gamma, y, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rms_norm(const void* ids, int ids_bytes, const uint16_t* table, const uint16_t* gamma,
+                                 uint16_t* y, uint16_t* hidden, int rows, int cols, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(embed_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, ids, ids_bytes, table, gamma, y,
+                     hidden, cols, eps);
   return hipGetLastError();
 }
 

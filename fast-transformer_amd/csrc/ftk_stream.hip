@@ -59,12 +59,16 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   // ---- this lane's slice of x (and of the gain): small, mostly cache hits ---
   // Issued first: loads complete in issue order, so the prologue below waits
   // for these and not for the weight batch issued after them.
+  // With the prologue, row m is x[m] or the gathered x[x_ids[m]], plus the residual.
+  const uint16_t* xrow[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xrow[m] = (PRO && m < M) ? x_row(a, m) : a.x + (size_t)m * K;
+  auto x_in = [&](int m, size_t k) { return PRO ? prologue_in(a, xrow[m], m, k) : load16(xrow[m] + k); };
   u32x4_t xr[MR][C];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int j = 0; j < C; ++j)
-      xr[m][j] = m < M ? load16(a.x + (size_t)m * K + first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int j = 0; j < C; ++j) xr[m][j] = m < M ? x_in(m, first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
   u32x4_t g[PRO ? C : 1];
   if constexpr (PRO) {
 #pragma unroll
@@ -97,10 +101,19 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
       } else {
         const int KC = K >> 3;
         if (m < M && tid < kThreads)
-          for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(load16(a.x + (size_t)m * K + (size_t)c * 8), ss);
+          for (int c = tid; c < KC; c += kThreads) ss = sum_squares8(x_in(m, (size_t)c * 8), ss);
       }
       const float s = wave_sum(ss);
       if (lane == 0 && wave < kWaves) red[m][wave] = s;
+    }
+    // The normalised rows themselves (x + residual) go out once, from workgroup 0
+    // (its first row group covers all of K).
+    if (a.sum != nullptr && blockIdx.x == 0 && grp == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M)
+#pragma unroll
+          for (int j = 0; j < C; ++j) store16(a.sum + (size_t)m * K + first + j * kStep, xr[m][j]);
     }
     __syncthreads();
 #pragma unroll

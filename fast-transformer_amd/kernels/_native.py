@@ -43,6 +43,12 @@ class Plan(ctypes.Structure):
                 ("workspace_bytes", _i64)]
 
 
+class Rows(ctypes.Structure):
+    """ftk_rows: the prologue's residual, stored sum and gathered row indices (NULL = absent)."""
+
+    _fields_ = [("residual", _c_void_p), ("sum", _c_void_p), ("x_ids", _c_void_p), ("x_ids_bytes", _int)]
+
+
 # name -> (restype, argtypes), exactly the declarations of include/ftk.h
 SIGNATURES = {
     "ftk_version": (ctypes.c_char_p, []),
@@ -58,7 +64,12 @@ SIGNATURES = {
                                        _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "ftk_project_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64, _int,
                                 _c_void_p, _int, _c_void_p, _c_void_p, _i64, ctypes.POINTER(Config), _c_void_p]),
+    "ftk_project_rows_bf16": (_int, [_c_void_p, ctypes.POINTER(Rows), _c_void_p, _float, _c_void_p, _c_void_p,
+                                     _i64, _i64, _i64, _int, _c_void_p, _int, _c_void_p, _c_void_p, _i64,
+                                     ctypes.POINTER(Config), _c_void_p]),
     "ftk_rms_norm_bf16": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _float, _c_void_p]),
+    "ftk_embed_rms_norm_bf16": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                                       _float, _c_void_p]),
     "ftk_add_rms_norm_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
                                      _i64, _float, _c_void_p]),
     "ftk_swiglu_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _i64, _i64, _c_void_p]),

@@ -40,34 +40,38 @@ def argmax(logits, block=8192, top=None):
 
 
 def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None, ids_dtype=torch.int64,
-                   config=None):
-    """(ids, logits or None): greedy ids of rms_norm?(x) @ weight.T in one projection kernel.
+                   config=None, residual=None):
+    """(ids, logits or None): greedy ids of rms_norm?(x [+ residual]) @ weight.T in one projection kernel.
 
-    Ties go to the lowest index of the BF16-rounded logits. Shapes the fused
-    kernel does not take run the norm, projection and argmax kernels in turn.
+    Ties go to the lowest index of the BF16-rounded logits. ``residual`` makes
+    the prologue the final add_rms_norm of engine/decode.py:264-265 (its sum is
+    not needed afterwards). Shapes the fused kernel does not take run the norm,
+    projection and argmax kernels in turn.
     """
-    _native.require_gpu(x, weight, norm_weight, top)
+    _native.require_gpu(x, weight, norm_weight, top, residual)
+    if residual is not None and norm_weight is None:
+        raise ValueError("a residual needs the norm it feeds (norm_weight)")
+    from kernels.linear import fused_project, linear
+    from kernels.rmsnorm import add_rms_norm, rms_norm
+
     shape = x.shape
     flat = x.reshape(-1, shape[-1]).contiguous()
     m, k = flat.shape
     v = weight.shape[0]
     ids = torch.empty(shape[:-1], dtype=ids_dtype, device=x.device)
     out = torch.empty((*shape[:-1], v), dtype=torch.bfloat16, device=x.device) if logits else None
-    ws = _native.project_workspace(x.device, m, v, k, _native.EPI_ARGMAX, config, prologue=norm_weight is not None)
-    ids_bytes = {torch.int64: 8, torch.int32: 4}[ids_dtype]
-    status = _native.try_call(
-        "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
-        _native.ptr(out), m, v, k, _native.EPI_ARGMAX, _native.ptr(ids), ids_bytes, _native.ptr(top),
-        _native.ptr(ws), ws.numel(), config, _native.stream_of(flat))
-    if status == _native.FTK_ERR_UNSUPPORTED:
-        from kernels.linear import linear
-        from kernels.rmsnorm import rms_norm
-
-        xn = x if norm_weight is None else rms_norm(x, norm_weight, eps)
+    if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < m):
+        raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
+    res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
+    status = fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
+                           config=config)
+    if status != _native.FTK_OK:
+        if residual is not None:
+            xn = add_rms_norm(x, residual, norm_weight, eps)[0]
+        else:
+            xn = x if norm_weight is None else rms_norm(x, norm_weight, eps)
         full = linear(xn, weight)
         return argmax(full, top=top).to(ids_dtype), (full if logits else None)
-    if status != _native.FTK_OK:
-        raise _native.FtkError("ftk_project_bf16", status)
     return ids, out
 
 

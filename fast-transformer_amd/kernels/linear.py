@@ -19,6 +19,7 @@ Beyond the reference's surface, the fused forms of the path live here too:
 argmax.py the SwiGLU and greedy-argmax epilogues.
 """
 
+import ctypes
 import os
 import statistics
 
@@ -43,6 +44,34 @@ def _as_rows(x):
     return x.reshape(rows, x.shape[-1]).contiguous()
 
 
+def fused_project(x, weight, epilogue, out, norm_weight=None, eps=1e-6, residual=None, x_ids=None, summed=None,
+                  ids=None, top=None, config=None):
+    """One projection launch with its fused prologue / epilogue (ftk_project_rows_bf16).
+
+    ``x`` is [M, K] (or, with ``x_ids``, the [rows, K] table they index);
+    ``residual`` [M, K] is added before the norm and ``summed`` [M, K] receives
+    the rows the norm read. Returns the C status: FTK_OK, or
+    FTK_ERR_UNSUPPORTED when the shape / alignment has no fused kernel (the
+    caller then composes the separate kernels). Raises on anything else.
+    """
+    m = x_ids.numel() if x_ids is not None else x.shape[0]
+    k = x.shape[1]
+    n = weight.shape[0]
+    rows = None
+    if residual is not None or summed is not None or x_ids is not None:
+        ids_bytes = 0 if x_ids is None else {torch.int64: 8, torch.int32: 4}[x_ids.dtype]
+        rows = ctypes.byref(_native.Rows(_native.ptr(residual), _native.ptr(summed), _native.ptr(x_ids), ids_bytes))
+    ws = _native.project_workspace(x.device, m, n, k, epilogue, config, prologue=norm_weight is not None)
+    ids_bytes = 0 if ids is None else {torch.int64: 8, torch.int32: 4}[ids.dtype]
+    status = _native.try_call(
+        "ftk_project_rows_bf16", _native.ptr(x), rows, _native.ptr(norm_weight), float(eps), _native.ptr(weight),
+        _native.ptr(out), m, n, k, epilogue, _native.ptr(ids), ids_bytes, _native.ptr(top), _native.ptr(ws),
+        ws.numel(), config, _native.stream_of(x))
+    if status not in (_native.FTK_OK, _native.FTK_ERR_UNSUPPORTED):
+        raise _native.FtkError("ftk_project_rows_bf16", status)
+    return status
+
+
 def project(x, weight, config=None, out=None):
     """y[M, N] = x[M, K] @ weight[N, K].T on the GPU (the device work of _project, linear.py:178-314).
 
@@ -60,16 +89,13 @@ def project(x, weight, config=None, out=None):
         raise ValueError(f"x has K={k}, weight has K={weight.shape[1]}")
     if out is None:
         out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
-    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config)
-    status = _native.try_call("ftk_project_bf16", _native.ptr(x), None, 0.0, _native.ptr(weight), _native.ptr(out),
-                              m, n, k, _native.EPI_STORE, None, 0, None, _native.ptr(ws), ws.numel(), config,
-                              _native.stream_of(x))
-    if status == _native.FTK_ERR_UNSUPPORTED and config is None:
+    status = fused_project(x, weight, _native.EPI_STORE, out, config=config)
+    if status == _native.FTK_ERR_UNSUPPORTED:
+        if config is not None:
+            raise _native.FtkError("ftk_project_rows_bf16", status)
         # unaligned pointers: the generic kind takes any alignment
         _native.call("ftk_linear_bf16", _native.ptr(x), _native.ptr(weight), _native.ptr(out), m, n, k,
                      _native.stream_of(x))
-    elif status != _native.FTK_OK:
-        raise _native.FtkError("ftk_project_bf16", status)
     return out
 
 
@@ -77,8 +103,8 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
     """rms_norm(x, norm_weight, eps) @ weight.T with the norm folded into the projection's prologue.
 
     Cast order of engine/kernels/rmsnorm.py:35-46 (normalised value rounded to
-    BF16 before the gain multiply). Shapes the fused kernel does not take
-    (K % 8 != 0, unaligned, M > 4) run the separate norm kernel, then ``linear``.
+    BF16 before the gain multiply). Shapes no fused kernel takes (K % 8 != 0,
+    unaligned) run the separate norm kernel, then ``linear``.
     """
     _native.require_gpu(x, norm_weight, weight)
     shape = x.shape
@@ -86,17 +112,58 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
     m, k = flat.shape
     n = weight.shape[0]
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
-    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_STORE, config, prologue=True)
-    status = _native.try_call(
-        "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(weight),
-        _native.ptr(out), m, n, k, _native.EPI_STORE, None, 0, None, _native.ptr(ws), ws.numel(), config,
-        _native.stream_of(flat))
-    if status == _native.FTK_ERR_UNSUPPORTED:
+    if fused_project(flat, weight, _native.EPI_STORE, out, norm_weight, eps, config=config) != _native.FTK_OK:
         from kernels.rmsnorm import rms_norm
         return linear(rms_norm(x, norm_weight, eps), weight)
-    if status != _native.FTK_OK:
-        raise _native.FtkError("ftk_project_bf16", status)
     return out.reshape(*shape[:-1], n)
+
+
+def add_rms_norm_linear(x, residual, norm_weight, eps, weight, config=None):
+    """(add_rms_norm(x, residual)[0] @ weight.T, x + residual) in one launch.
+
+    The residual side of the prologue (engine/kernels/rmsnorm.py:75-125, the
+    calls at engine/decode.py:240-261): s = bf16(x + residual) is normalised
+    and projected, and s is returned as the next residual. Inputs are not
+    modified. Shapes without a fused kernel run add_rms_norm, then ``linear``.
+    """
+    _native.require_gpu(x, residual, norm_weight, weight)
+    if tuple(x.shape) != tuple(residual.shape):
+        raise ValueError("x and residual must have the same shape")
+    shape = x.shape
+    flat, res = _as_rows(x), _as_rows(residual)
+    m, k = flat.shape
+    n = weight.shape[0]
+    out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    summed = torch.empty_like(res)
+    status = fused_project(flat, weight, _native.EPI_STORE, out, norm_weight, eps, residual=res, summed=summed,
+                           config=config)
+    if status != _native.FTK_OK:
+        from kernels.rmsnorm import add_rms_norm
+        normed, summed = add_rms_norm(x, residual, norm_weight, eps)
+        return linear(normed, weight), summed
+    return out.reshape(*shape[:-1], n), summed.reshape(shape)
+
+
+def embed_rms_norm_linear(token_ids, table, norm_weight, eps, weight, config=None):
+    """(embed_rms_norm(token_ids, table)[0] @ weight.T, the embedding rows) in one launch.
+
+    The first layer's input (engine/kernels/rmsnorm.py:128-162, engine/decode.py:229):
+    row m = table[token_ids[m]], normalised and projected; the gathered rows are
+    returned as the residual stream. ``token_ids`` int64 or int32.
+    """
+    _native.require_gpu(token_ids, table, norm_weight, weight)
+    ids = token_ids.reshape(-1).contiguous()
+    k = table.shape[1]
+    n = weight.shape[0]
+    out = torch.empty((ids.numel(), n), device=table.device, dtype=torch.bfloat16)
+    hidden = torch.empty((ids.numel(), k), device=table.device, dtype=torch.bfloat16)
+    status = fused_project(table.contiguous(), weight, _native.EPI_STORE, out, norm_weight, eps, x_ids=ids,
+                           summed=hidden, config=config)
+    if status != _native.FTK_OK:
+        from kernels.rmsnorm import embed_rms_norm
+        normed, hidden = embed_rms_norm(token_ids, table, norm_weight, eps)
+        return linear(normed, weight), hidden
+    return out.reshape(*token_ids.shape, n), hidden.reshape(*token_ids.shape, k)
 
 
 def _candidates(m, n, k):
@@ -109,10 +176,22 @@ def _candidates(m, n, k):
                                 (2, 4, 2), (1, 1, 4), (2, 1, 4), (2, 2, 4)):
             for gpc in (4, 8, 16):
                 configs.append(_native.Config(_native.KIND_GEMV, rpw, unroll, gpc, kw))
+    for rpw in (2, 4, 8):
+        for kw in (1, 2, 4, 8):
+            for gpc in (2, 4, 16, 32):
+                configs.append(_native.Config(_native.KIND_STREAM, rpw, 0, gpc, kw))
+    for rows in (16, 32):
+        for kw in (8, 16):
+            for unroll in (2, 4, 8, 16):
+                for gpc in (1, 2):
+                    configs.append(_native.Config(_native.KIND_MFMA_STREAM, rows, unroll, gpc, kw))
     for rows, unroll, waves in ((16, 4, 4), (16, 8, 4), (16, 4, 8), (16, 8, 8), (16, 4, 16), (32, 4, 4),
                                 (32, 8, 4), (32, 4, 8), (32, 8, 8), (32, 4, 16), (64, 2, 4), (64, 4, 4), (64, 2, 8)):
         configs.append(_native.Config(_native.KIND_MFMA, rows, unroll, 0, waves))
-    return configs
+    # only launch shapes the planner accepts for this problem
+    p = _native.Plan()
+    return [c for c in configs
+            if c is None or _native.lib().ftk_plan_project(m, n, k, _native.EPI_STORE, 256, c, p) == _native.FTK_OK]
 
 
 def _time(fn, reps=20):

@@ -1,12 +1,15 @@
 """Qwen3 RMSNorm with the reference's BF16 cast boundaries (engine/kernels/rmsnorm.py:1-162).
 
-``rms_norm(x, weight, eps)`` and ``add_rms_norm(x, residual, weight, eps)`` keep
+``rms_norm(x, weight, eps)``, ``add_rms_norm(x, residual, weight, eps)`` and
+``embed_rms_norm(token_ids, table, weight, eps)`` keep
 the reference's signatures, errors and outputs: the normalised value is rounded
 to BF16 before the gain multiply (rmsnorm.py:35-46), the residual sum is a
 BF16 add (rmsnorm.py:86-95), inputs are never mutated. ``add_rms_norm``
 accepts a ``Split`` like the reference. The fused RMSNorm prologue of the
-projections is ``kernels.linear.rms_norm_linear`` and the ``norm_weight``
-arguments of ``kernels.swiglu.gate_up_swiglu`` / ``kernels.argmax.lm_head_argmax``.
+projections is ``kernels.linear.rms_norm_linear`` (with the residual side:
+``add_rms_norm_linear``, ``embed_rms_norm_linear``) and the ``norm_weight`` /
+``residual`` arguments of ``kernels.swiglu.gate_up_swiglu`` /
+``kernels.argmax.lm_head_argmax``.
 """
 
 import torch
@@ -50,3 +53,22 @@ def add_rms_norm(x, residual, weight, eps):
                  count if splits > 1 else 0, _native.ptr(residual_rows), _native.ptr(weight.contiguous()),
                  _native.ptr(out), _native.ptr(summed), rows, width, float(eps), _native.stream_of(residual_rows))
     return out.reshape(shape), summed.reshape(shape)
+
+
+def embed_rms_norm(token_ids, table, weight, eps):
+    """(normalized, hidden) for the embedding rows of ``token_ids`` in one launch (rmsnorm.py:145-162).
+
+    ``hidden`` is the gathered rows (the residual stream), ``normalized`` their
+    RMSNorm. int64 ids and a contiguous table, as the reference requires.
+    """
+    _native.require_gpu(token_ids, table, weight)
+    ids = token_ids.reshape(-1).contiguous()
+    if not table.is_contiguous() or ids.dtype != torch.int64:
+        raise ValueError("embedding rows must fit one block and the table must be contiguous")
+    n_cols = table.shape[1]
+    hidden = torch.empty((ids.numel(), n_cols), dtype=table.dtype, device=table.device)
+    out = torch.empty_like(hidden)
+    _native.call("ftk_embed_rms_norm_bf16", _native.ptr(ids), 8, _native.ptr(table), _native.ptr(weight.contiguous()),
+                 _native.ptr(out), _native.ptr(hidden), ids.numel(), n_cols, float(eps), _native.stream_of(table))
+    shape = (*token_ids.shape, n_cols)
+    return out.reshape(shape), hidden.reshape(shape)

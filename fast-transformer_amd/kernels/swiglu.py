@@ -29,9 +29,18 @@ def swiglu(packed):
     return output
 
 
-def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None):
-    """swiglu(rms_norm?(x) @ gate_up_weight.T) in one projection kernel; [..., I] BF16."""
-    _native.require_gpu(x, gate_up_weight, norm_weight)
+def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, residual=None):
+    """swiglu(rms_norm?(x [+ residual]) @ gate_up_weight.T) in one projection kernel; [..., I] BF16.
+
+    With ``residual`` the prologue is add_rms_norm (engine/kernels/rmsnorm.py:75-125,
+    the post-attention norm of engine/decode.py:258-261) and the result is
+    ``(activation, x + residual)``: the sum is the next residual stream.
+    """
+    _native.require_gpu(x, gate_up_weight, norm_weight, residual)
+    if residual is not None and norm_weight is None:
+        raise ValueError("a residual needs the norm it feeds (norm_weight)")
+    from kernels.linear import fused_project, linear
+
     shape = x.shape
     flat = x.reshape(-1, shape[-1]).contiguous()
     m, k = flat.shape
@@ -39,16 +48,16 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None):
     if n % 2:
         raise ValueError("gate_up_weight must stack gate and up rows: an even row count")
     out = torch.empty((m, n // 2), device=x.device, dtype=torch.bfloat16)
-    ws = _native.project_workspace(x.device, m, n, k, _native.EPI_SWIGLU, config, prologue=norm_weight is not None)
-    status = _native.try_call(
-        "ftk_project_bf16", _native.ptr(flat), _native.ptr(norm_weight), float(eps), _native.ptr(gate_up_weight),
-        _native.ptr(out), m, n, k, _native.EPI_SWIGLU, None, 0, None, _native.ptr(ws), ws.numel(), config,
-        _native.stream_of(flat))
-    if status == _native.FTK_ERR_UNSUPPORTED:
-        from kernels.linear import linear
-        from kernels.rmsnorm import rms_norm
+    res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
+    summed = None if residual is None else torch.empty_like(res)
+    status = fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
+                           summed=summed, config=config)
+    if status != _native.FTK_OK:
+        from kernels.rmsnorm import add_rms_norm, rms_norm
+        if residual is not None:
+            xn, summed = add_rms_norm(x, residual, norm_weight, eps)
+            return swiglu(linear(xn, gate_up_weight)), summed
         xn = x if norm_weight is None else rms_norm(x, norm_weight, eps)
         return swiglu(linear(xn, gate_up_weight))
-    if status != _native.FTK_OK:
-        raise _native.FtkError("ftk_project_bf16", status)
-    return out.reshape(*shape[:-1], n // 2)
+    act = out.reshape(*shape[:-1], n // 2)
+    return act if residual is None else (act, summed.reshape(shape))

@@ -146,6 +146,27 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
                      int64_t K, int epilogue, void* ids, int ids_bytes, float* top, void* workspace,
                      int64_t workspace_bytes, const ftk_config* cfg, void* stream);
 
+/* The prologue's input rows beyond a plain x: the residual side of the norm
+ * (engine/kernels/rmsnorm.py:75-125 add_rms_norm, called at engine/decode.py:240-261)
+ * and the embedding gather of the first layer (rmsnorm.py:128-162 embed_rms_norm,
+ * decode.py:229). The norm then reads s[m] = bf16(xrow(m) + residual[m]) (no add
+ * without a residual), xrow(m) = x[x_ids[m]] (x a [rows, K] table) or x[m], and
+ * s is stored into `sum` when non-NULL: the BF16 residual stream the next layer
+ * adds to. `sum` must not overlap x, residual or y. */
+typedef struct ftk_rows {
+  const void* residual;  /* [M, K] BF16, or NULL */
+  void* sum;             /* [M, K] BF16 out, or NULL */
+  const void* x_ids;     /* [M] row indices into x, or NULL */
+  int x_ids_bytes;       /* 4 (int32) or 8 (int64) */
+} ftk_rows;
+
+/* ftk_project_bf16 with the prologue's rows described by `rows` (NULL: x as is).
+ * Needs gamma. Kinds without the fused form return FTK_ERR_UNSUPPORTED (the
+ * generic kind; the MFMA kind when sum is NULL). */
+int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma, float eps, const void* w, void* y,
+                          int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
+                          void* workspace, int64_t workspace_bytes, const ftk_config* cfg, void* stream);
+
 /* ---- standalone operators ---------------------------------------------------- */
 
 /* rms_norm(x, weight, eps) (engine/kernels/rmsnorm.py:49-72): x rows of
@@ -159,6 +180,11 @@ int ftk_rms_norm_bf16(const void* x, int64_t row_stride, const void* gamma, void
  * (engine/kernels/merged.py:13-45). Writes y (normalized) and sum (BF16 x + r). */
 int ftk_add_rms_norm_bf16(const void* x, int x_splits, int64_t x_split_stride, const void* residual,
                           const void* gamma, void* y, void* sum, int64_t rows, int64_t cols, float eps, void* stream);
+
+/* embed_rms_norm(token_ids, table, weight, eps) (engine/kernels/rmsnorm.py:145-162):
+ * hidden[r] = table[ids[r]] (the residual stream), y[r] = rms_norm(hidden[r]). */
+int ftk_embed_rms_norm_bf16(const void* ids, int ids_bytes, const void* table, const void* gamma, void* y,
+                            void* hidden, int64_t rows, int64_t cols, float eps, void* stream);
 
 /* swiglu(packed) (engine/kernels/swiglu.py:27-40): packed [rows, 2*width] BF16
  * (splits = 0) or FP32 split partials; out [rows, width]. */

@@ -88,6 +88,16 @@ def add_rms_norm(x_bits, residual_bits, gamma_bits, eps):
     return rms_norm(summed, gamma_bits, eps), summed
 
 
+def embed_rms_norm(token_ids, table_bits, gamma_bits, eps):
+    """(normalised, hidden): hidden = table[token_ids] (the residual stream), then rms_norm(hidden).
+
+    (engine/kernels/rmsnorm.py:128-162: the gathered row is stored unchanged and
+    normalised with the cast order of :35-46.)
+    """
+    hidden = np.asarray(table_bits)[np.asarray(token_ids, dtype=np.int64)]
+    return rms_norm(hidden, gamma_bits, eps), hidden
+
+
 def silu_bf16(g):
     """bf16( g / (1 + exp(-g)) ) for FP32 g, every step an FP32 operation.
 
@@ -148,6 +158,13 @@ def lm_head_argmax(x_bits, w_bits, gamma_bits=None, eps=1e-6):
 def norm_project(x_bits, gamma_bits, eps, w_bits):
     """rms_norm prologue then projection: the QKV / lm_head input path of engine/decode.py:240-278."""
     return project(rms_norm(x_bits, gamma_bits, eps), w_bits)
+
+
+def add_norm_project(x_bits, residual_bits, gamma_bits, eps, w_bits):
+    """(projection of add_rms_norm(x, r), the BF16 sum): the residual side of the prologue
+    (engine/decode.py:240-261 add_rms_norm then the layer's projection)."""
+    normed, summed = add_rms_norm(x_bits, residual_bits, gamma_bits, eps)
+    return project(normed, w_bits), summed
 
 
 def gate_up_swiglu(x_bits, w_bits, gamma_bits=None, eps=1e-6):

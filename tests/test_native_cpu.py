@@ -61,6 +61,18 @@ def test_invalid_arguments_rejected_before_any_launch():
     assert lib.ftk_project_bf16(fake, None, 0.0, fake, None, 1, 64, 64, _native.EPI_ARGMAX, fake, 8, None, None, 0,
                                 None, None) in (_native.FTK_ERR_WORKSPACE, _native.FTK_ERR_HIP)
     assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 3, None, fake, 64, None) == _native.FTK_ERR_INVALID
+    # the prologue's stored rows may not alias its inputs or outputs, and need the norm
+    buf = ctypes.c_void_p(4096)
+    rows = _native.Rows(buf, buf, None, 0)
+    assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64, 64,
+                                     0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
+    rows = _native.Rows(buf, ctypes.c_void_p(8192), None, 0)
+    assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), None, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64, 64,
+                                     0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
+    rows = _native.Rows(None, None, fake, 3)
+    assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64, 64,
+                                     0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_embed_rms_norm_bf16(fake, 3, fake, fake, fake, fake, 1, 8, 1e-6, None) == _native.FTK_ERR_INVALID
 
 
 @pytest.mark.parametrize("m", [0, 33])

@@ -125,6 +125,20 @@ def test_add_rms_norm_matches_module_on_bf16_sum(shape):
     assert _ulps(y, data[f"ysum_{key}"]).max() <= 2
 
 
+def test_embed_rms_norm_gathers_like_torch_embedding():
+    """hidden = torch's embedding lookup of the same table (an independent gather); the norm is rms_norm's."""
+    rng = np.random.default_rng(11)
+    table = bf16.round_bits(rng.standard_normal((50, 96)).astype(np.float32))
+    gamma = bf16.round_bits(1 + 0.1 * rng.standard_normal(96).astype(np.float32))
+    ids = np.array([[3, 49, 0], [7, 7, 12]], dtype=np.int64)
+    y, hidden = path.embed_rms_norm(ids, table, gamma, 1e-6)
+    want = F.embedding(torch.from_numpy(ids), from_bits(table)).contiguous()
+    assert np.array_equal(hidden, to_bits(want))
+    assert np.array_equal(y, path.rms_norm(hidden, gamma, 1e-6))
+    # consecutive ids reproduce the table itself
+    assert np.array_equal(path.embed_rms_norm(np.arange(50), table, gamma, 1e-6)[1], table)
+
+
 def test_rms_norm_wrong_cast_detector():
     """Keeping x_hat * gamma in FP32 is a different function (verify_gpu.py:56-61): >5% of outputs differ."""
     data = _load("rmsnorm.npz")
@@ -199,6 +213,10 @@ def test_fused_forms_compose():
     xn = path.rms_norm(x, gamma, 1e-6)
     assert np.array_equal(path.gate_up_swiglu(x, w, gamma, 1e-6), path.swiglu(path.project(xn, w)))
     assert np.array_equal(path.norm_project(x, gamma, 1e-6, w), path.project(xn, w))
+    r = bf16.round_bits(rng.standard_normal((2, 64)).astype(np.float32))
+    y, s = path.add_norm_project(x, r, gamma, 1e-6, w)
+    normed, summed = path.add_rms_norm(x, r, gamma, 1e-6)
+    assert np.array_equal(s, summed) and np.array_equal(y, path.project(normed, w))
 
 
 def test_oracle_matches_torch_cpu_path():
