@@ -228,6 +228,11 @@ def kernel_name(plan, prologue, epilogue):
     return f"ftk::{head}, PRO={int(prologue)}, {epilogue}> grid {plan.grid}"
 
 
+def stage(msg):
+    """One progress line per finished stage (stderr; the JSON result stays the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def load_traffic():
     f = ROOT / "profiles" / "traffic_gate_up_swiglu_8b_m1.json"
     if f.exists():
@@ -262,9 +267,11 @@ def main():
         profile_gate_up(cfg, dev, args.profile_gate_up)
         return
     model = Model(cfg, dev)
+    stage("Qwen3-8B weights resident")
     step = Step(model, 1, dev)
     graph = capture(step.run)
     layer_graph = capture(step.layers)
+    stage("decode step captured")
 
     for _ in range(args.warmup):
         graph.replay()
@@ -295,6 +302,7 @@ def main():
                 "avg_launch_us": round(gu_us, 3)}
 
     per_shape = {}
+    stage(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
     if not args.no_shapes:
         per_shape = shapes_table(model, step, dev)
 
@@ -349,6 +357,7 @@ def shapes_table(model8, step8, dev):
     for kind in ("qkv", "o", "gate_up", "down"):
         us = per_kind(step8, kind)
         out[f"C3 8B {kind} M=1"] = shape_entry(us, lb[kind])
+    stage("C3 per-projection timings done")
     # C5: lm_head + argmax at M=1 and M=5
     for m in (1, 5):
         st = step8 if m == 1 else Step(model8, m, dev, seed=5)
@@ -356,6 +365,7 @@ def shapes_table(model8, step8, dev):
         g = capture(lambda: A.lm_head_argmax(h, model8.head, model8.final_norm, EPS, logits=True, top=st.top))
         us = time_graph(g)
         out[f"C5 lm_head+argmax M={m}"] = shape_entry(us, head_bytes(cfg, m), 2 * m * cfg["vocab"] * cfg["hidden"])
+        stage(f"C5 M={m} done")
     # C4: 8B layer set at M = 5, 8, 16
     for m in (5, 8, 16):
         st = Step(model8, m, dev, seed=m)
@@ -364,6 +374,7 @@ def shapes_table(model8, step8, dev):
         byts = sum(layer_bytes(cfg, m).values())
         flops = 2 * m * sum(n * k for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)))
         out[f"C4 8B layer M={m}"] = shape_entry(us, byts, flops)
+        stage(f"C4 M={m} done")
     # C3 per layer (M=1)
     g = capture(step8.layers)
     us = time_graph(g, reps=5) / cfg["layers"]

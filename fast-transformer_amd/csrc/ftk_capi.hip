@@ -111,6 +111,35 @@ static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, i
   return {0, 0, 0};
 }
 
+// QUAD launch shape, from the M = 1..16 sweep of the Qwen3-8B shapes on MI355X:
+// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets)
+// and for lm_head from 5 rows, 8 otherwise; the first shape that fits the
+// registers (with the prologue at 9..16 rows, 4 rows per tile).
+struct QuadDefault {
+  int rows, kw;
+};
+static QuadDefault quad_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
+  if (M < 1 || M > kQuadMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  const int want = (epi == FTK_EPI_SWIGLU || (epi == FTK_EPI_ARGMAX && M > 4)) ? 16 : 8;
+  const QuadDefault order[] = {{want, 8}, {8, 8}, {4, 8}, {want, 4}, {8, 4}, {4, 4}, {8, 16}};
+  for (const QuadDefault& d : order)
+    if (quad_supported((int)M, d.rows, (int)K, d.kw, epi, pro)) return d;
+  return {0, 0};
+}
+// QUAD grid cap: one workgroup per CU walking several tiles (their prologue is
+// paid once); lm_head at up to 4 rows as shallow walks of many workgroups.
+static int64_t quad_default_cap(int64_t M, int tiles, int cus) {
+  return (tiles > 8192 && M <= 4) ? 32LL * cus : (int64_t)cus;
+}
+// Where QUAD beats STREAM below 5 rows (MI355X, Qwen3-8B shapes): lm_head from 2
+// rows, SwiGLU from 3, any projection with the prologue at 4.
+static bool quad_preferred(int64_t M, int epi, bool pro) {
+  if (M >= 5) return true;
+  if (epi == FTK_EPI_ARGMAX) return M >= 2;
+  if (epi == FTK_EPI_SWIGLU) return M >= 3;
+  return pro && M >= 4;
+}
+
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
 
@@ -127,8 +156,14 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (epi == FTK_EPI_SWIGLU && (N % 2)) return FTK_ERR_INVALID;
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
   if (kind == FTK_KIND_AUTO) {
+    // Measured on MI355X at the Qwen3-8B shapes: STREAM (v_dot2) at M = 1 and,
+    // up to M = 4, where quad_preferred says so; QUAD (4x4x4 MFMA blocks) for
+    // M = 5..8; MFMA_STREAM (16x16x32) beyond.
+    const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     if (K % 8)
       kind = FTK_KIND_GENERIC;
+    else if (M <= 8 && quad && quad_preferred(M, epi, pro))
+      kind = FTK_KIND_QUAD;
     else if (M <= 4 && stream_default(M, epi, N, K).rpw)
       kind = FTK_KIND_STREAM;
     else if (M <= 4)
@@ -197,6 +232,27 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
                                                   : stream_default_cap(p->tiles, cus);
+    const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
+    const int64_t units = cap > floor ? cap : floor;
+    p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
+    return FTK_OK;
+  }
+  if (kind == FTK_KIND_QUAD) {
+    if (M > kQuadMaxRows) return FTK_ERR_UNSUPPORTED;
+    const QuadDefault d = quad_default(M, epi, pro, N, K);
+    const int kw = cfg && cfg->waves ? cfg->waves : d.kw;
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : d.rows;
+    const int c = quad_segments((int)K, kw);
+    if (c == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
+    if (!quad_supported((int)M, rows, (int)K, kw, epi, pro)) return FTK_ERR_INVALID;
+    p->rows_per_wave = rows;
+    p->unroll = c;
+    p->waves = kw;
+    p->threads = 64 * stream_waves(kw);
+    p->tiles = gemv_tiles(epi, (int)N, rows, kw);
+    const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
+                                                  : quad_default_cap(M, p->tiles, cus);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
@@ -352,9 +408,10 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
       }
     return FTK_OK;
   }
-  if (p->kind != FTK_KIND_GEMV && p->kind != FTK_KIND_STREAM) return FTK_ERR_UNSUPPORTED;
+  if (p->kind != FTK_KIND_GEMV && p->kind != FTK_KIND_STREAM && p->kind != FTK_KIND_QUAD) return FTK_ERR_UNSUPPORTED;
   if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
-  if (p->kind == FTK_KIND_STREAM && (p->tiles + p->grid - 1) / p->grid > kStreamMaxTiles) return FTK_ERR_INVALID;
+  if ((p->kind == FTK_KIND_STREAM || p->kind == FTK_KIND_QUAD) && (p->tiles + p->grid - 1) / p->grid > kStreamMaxTiles)
+    return FTK_ERR_INVALID;
   const int pw = gemv_per_wave(epilogue, p->rows_per_wave);
   const int groups = gemv_groups(p->waves);
   const int halves = epilogue == FTK_EPI_SWIGLU ? 2 : 1;
@@ -446,6 +503,9 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
   } else if (p.kind == FTK_KIND_MFMA_STREAM) {
     MstreamShape g = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid, p.tiles};
     e = launch_mstream(a, epilogue, g, s);
+  } else if (p.kind == FTK_KIND_QUAD) {
+    QuadShape g = {p.rows_per_wave, p.waves, p.grid, p.tiles};
+    e = launch_quad(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);

@@ -13,6 +13,7 @@ namespace ftk {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -33,9 +34,20 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return u >> 16;
 }
 
-// FP32 -> nearest BF16 value, kept in FP32 (one rounding).
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// Two FP32 values rounded to nearest-even BF16, packed (lo in the low half),
+// by the compiler's float -> bfloat conversion (one v_cvt_pk_bf16_f32 on
+// gfx950). Finite values and infinities round exactly as f32_to_bf16; a NaN
+// stays a NaN with an unspecified payload, so this is only for values that
+// feed further arithmetic: stored results go through f32_to_bf16.
+__device__ __forceinline__ uint32_t rne_pair(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 
+// FP32 -> nearest BF16 value, kept in FP32 (one rounding; an intermediate).
+__device__ __forceinline__ float round_bf16(float f) { return lo_f32(rne_pair(f, 0.f)); }
+
+// A stored BF16 pair: round-to-nearest-even, every NaN as 0x7FC0.
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
 }
@@ -70,16 +82,15 @@ __device__ __forceinline__ float sum_squares8(u32x4_t v, float ss) {
 }
 
 // RMSNorm of 8 BF16 values: bf16(bf16(x * scale) * gain), the cast order of
-// engine/kernels/rmsnorm.py:35-46.
+// engine/kernels/rmsnorm.py:35-46. The result feeds the projection only.
 __device__ __forceinline__ u32x4_t norm8(u32x4_t v, u32x4_t g, float scale) {
   const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
   const uint32_t ge[4] = {g[0], g[1], g[2], g[3]};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float nlo = round_bf16(lo_f32(e[i]) * scale);
-    const float nhi = round_bf16(hi_f32(e[i]) * scale);
-    o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
+    const uint32_t n = rne_pair(lo_f32(e[i]) * scale, hi_f32(e[i]) * scale);
+    o[i] = rne_pair(lo_f32(n) * lo_f32(ge[i]), hi_f32(n) * hi_f32(ge[i]));
   }
   return u32x4_t{o[0], o[1], o[2], o[3]};
 }

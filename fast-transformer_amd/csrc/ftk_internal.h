@@ -89,6 +89,16 @@ struct MstreamShape {
 bool mstream_supported(int M, int t, int K, int kw, int unroll, int epi, bool pro);
 hipError_t launch_mstream(const ProjArgs& a, int epi, const MstreamShape& shape, hipStream_t stream);
 
+// Launch shape of the QUAD kind (K = 128 C KW, 4x4x4 MFMA blocks).
+struct QuadShape {
+  int rows;      // weight rows per row group per tile (4 RS; a multiple of 8 for SwiGLU)
+  int kw;        // waves per row group, splitting K (4, 8, 16)
+  int grid;      // workgroups; each walks ceil(tiles / grid) <= kStreamMaxTiles tiles
+  int tiles;
+};
+bool quad_supported(int M, int rows, int K, int kw, int epi, bool pro);
+hipError_t launch_quad(const ProjArgs& a, int epi, const QuadShape& shape, hipStream_t stream);
+
 // Launch shape of the MFMA kind.
 struct MfmaShape {
   int subtiles;  // T: 16-row MFMA subtiles per workgroup

@@ -110,17 +110,8 @@ __global__ __launch_bounds__(64 * W) void mfma_kernel(ProjArgs a, MfmaArgs p) {
         for (int mb = 0; mb < MB; ++mb) {
           u32x4_t b = xv[u][mb];
           if constexpr (PRO) {
-            const uint32_t e[4] = {b[0], b[1], b[2], b[3]};
-            const uint32_t ge[4] = {gv[u][0], gv[u][1], gv[u][2], gv[u][3]};
-            uint32_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              // bf16(x * rsqrt) first, then the gain multiply, rounded again.
-              const float nlo = round_bf16(lo_f32(e[i]) * sc[mb]);
-              const float nhi = round_bf16(hi_f32(e[i]) * sc[mb]);
-              o[i] = pack_bf16(nlo * lo_f32(ge[i]), nhi * hi_f32(ge[i]));
-            }
-            b = u32x4_t{o[0], o[1], o[2], o[3]};
+            // bf16(x * rsqrt) first, then the gain multiply, rounded again.
+            b = norm8(b, gv[u], sc[mb]);
           }
 #pragma unroll
           for (int t = 0; t < T; ++t) acc[t][mb] = mfma16x16x32(wv[u][t], b, acc[t][mb]);

@@ -107,6 +107,31 @@ FTK_HD int mstream_steps(int k, int kw) { return (kw < 1 || k % (32 * kw)) ? 0 :
 // Tiles a workgroup may walk: their per-wave partials wait in 64 KiB of LDS.
 FTK_HD int mstream_max_depth(int t, int kw) { return (64 * 1024) / (t * kw * 1024); }
 
+// ---- M = 2..16 with K = 128 C KW: the QUAD kind (4x4x4 MFMA blocks) --------
+// Same tiles, row groups and weight rows as the GEMV kind, with 4 RS weight
+// rows per row group per tile (rows_per_wave = 4 RS). Lane l = 4 b + i of wave
+// kw of a row group reads weight row i of each row set at K segment j KW + kw
+// (j < C), chunk b: elements 128 (j KW + kw) + 8 b .. + 7; it holds x rows
+// 4 q + i at the same elements. Workgroup b walks tiles b, b + grid, ... (at
+// most kStreamMaxTiles of them).
+
+constexpr int kQuadMaxRows = 16;
+// 128-element segments per lane per weight row (C), or 0 when K is not 128 C KW.
+FTK_HD int quad_segments(int k, int kw) { return (kw < 1 || k % (128 * kw)) ? 0 : k / (128 * kw); }
+// Groups of 4 x rows a kernel is built for: 1 (M <= 4), 2 (M <= 8), 4 (M <= 16).
+FTK_HD int quad_groups(int m) { return m < 1 ? 0 : m <= 4 ? 1 : m <= 8 ? 2 : m <= 16 ? 4 : 0; }
+// Whether a QUAD shape keeps its registers without spilling, estimated from the
+// gfx950 builds: the x slice (4 MQ C), the weight window (4 RS C), the
+// accumulators (4 RS MQ) and, with the prologue, what is live while it runs:
+// the residual, the gain and the normalisation's temporaries (6 MQ C + 4 C).
+// The cap is 248 registers (128 for a 16-wave workgroup); shapes over it are
+// not built.
+constexpr bool quad_fits(int mq, int rs, int c, int kw, bool pro) {
+  const int cap = kw >= 16 ? 128 : 248;
+  const int est = 4 * mq * c + 4 * rs * c + 4 * rs * mq + (pro ? 6 * mq * c + 4 * c : 0) + 32;
+  return est <= cap;
+}
+
 // ---- workspace layout of one projection call (bytes) -----------------------
 // Nothing in it carries state between calls: every slot a kernel reads was
 // written earlier in the same call (row scales by the prologue pass, argmax

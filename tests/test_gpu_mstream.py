@@ -116,12 +116,3 @@ def test_matches_mfma_kind_within_tolerance(cuda):
     a = L.rms_norm_linear(x, g, 1e-6, w, config=cfg(1, 16, 4))
     b = L.rms_norm_linear(x, g, 1e-6, w, config=_native.Config(_native.KIND_MFMA, 16, 4, 0, 16))
     assert within(to_bits(a), to_bits(b))
-
-
-def test_default_plan_for_8b_shapes(cuda):
-    for m in (5, 8, 16):
-        for n, k, epi, pro in ((6144, 4096, 0, True), (4096, 4096, 0, False), (24576, 4096, 1, True),
-                               (4096, 12288, 0, False), (151936, 4096, 2, True)):
-            # K = 12288 at M <= 8 runs the 8-row STREAM kernel (measured faster)
-            want = _native.KIND_STREAM if (k == 12288 and m <= 8) else _native.KIND_MFMA_STREAM
-            assert L.plan(m, n, k, epi, prologue=pro).kind == want, (m, n, k)

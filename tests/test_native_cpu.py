@@ -126,6 +126,28 @@ def _mstream_status(m, k, epilogue, t, kw, u):
     return _native.FTK_OK if (t, k // (32 * kw), kw, u) in _mstream_shapes(epilogue) else _native.FTK_ERR_INVALID
 
 
+#: (row sets RS, segments per lane C, KW) the QUAD kind may build (K = 128 C KW); single row sets
+#: only for store / argmax. A shape is built for a row count only where it fits the registers.
+QUAD_SHAPES = ((2, 8, 4), (4, 8, 4), (2, 4, 8), (4, 4, 8), (2, 12, 8), (2, 6, 16), (2, 2, 4), (2, 4, 4), (2, 6, 4))
+QUAD_ONE = ((1, 8, 4), (1, 4, 8), (1, 12, 8))
+
+
+def _quad_fits(mq, rs, c, kw, pro):
+    """The register estimate of the QUAD kind (x slice, weight window, accumulators, prologue inputs)."""
+    est = 4 * mq * c + 4 * rs * c + 4 * rs * mq + (6 * mq * c + 4 * c if pro else 0) + 32
+    return est <= (128 if kw >= 16 else 248)
+
+
+def _quad_status(m, k, epilogue, rows, kw, pro=False):
+    if m > 16 or k % (128 * kw):
+        return _native.FTK_ERR_UNSUPPORTED
+    mq = 1 if m <= 4 else 2 if m <= 8 else 4
+    c, rs = k // (128 * kw), rows // 4
+    shapes = QUAD_SHAPES + (() if epilogue == _native.EPI_SWIGLU else QUAD_ONE)
+    ok = rows % 4 == 0 and (rs, c, kw) in shapes and _quad_fits(mq, rs, c, kw, pro)
+    return _native.FTK_OK if ok else _native.FTK_ERR_INVALID
+
+
 def _configs(m):
     gemv = []
     if m <= 4:
@@ -138,6 +160,8 @@ def _configs(m):
     if m <= 16:
         gemv += [_native.Config(_native.KIND_MFMA_STREAM, 16 * t, u, gpc, kw)
                  for t, _, kw, u in MSTREAM_EVEN + MSTREAM_ONE for gpc in (1, 4)]
+        gemv += [_native.Config(_native.KIND_QUAD, 4 * rs, 0, gpc, kw)
+                 for rs, _, kw in QUAD_SHAPES + QUAD_ONE for gpc in (1, 8)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
             for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
     return [None] + gemv + mfma
@@ -153,7 +177,8 @@ def test_plan_writes_every_output_once(m, n, k):
             if cfg is not None and k % 8:
                 continue
             if (cfg is not None and epilogue == _native.EPI_SWIGLU
-                    and cfg.rows_per_wave in ((16,) if cfg.kind == _native.KIND_MFMA else (1,))):
+                    and cfg.rows_per_wave in ((16,) if cfg.kind == _native.KIND_MFMA
+                                              else (4,) if cfg.kind == _native.KIND_QUAD else (1,))):
                 continue  # a SwiGLU workgroup / row group needs a gate row and its up row
             p = _native.Plan()
             status = _native.lib().ftk_plan_project(m, n, k, epilogue, 256, cfg, p)
@@ -167,6 +192,11 @@ def test_plan_writes_every_output_once(m, n, k):
                     continue
             if cfg is not None and cfg.kind == _native.KIND_MFMA_STREAM:
                 want = _mstream_status(m, k, epilogue, cfg.rows_per_wave // 16, cfg.waves, cfg.unroll)
+                assert status == want, (m, n, k, epilogue, cfg)
+                if want != _native.FTK_OK:
+                    continue
+            if cfg is not None and cfg.kind == _native.KIND_QUAD:
+                want = _quad_status(m, k, epilogue, cfg.rows_per_wave, cfg.waves)
                 assert status == want, (m, n, k, epilogue, cfg)
                 if want != _native.FTK_OK:
                     continue
@@ -186,6 +216,9 @@ def test_plan_writes_every_output_once(m, n, k):
                 t = p.rows_per_wave // 16
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
                 assert p.threads == 64 * p.waves and k % (32 * p.waves) == 0
+            if p.kind == _native.KIND_QUAD:
+                assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
+                assert p.unroll * 128 * p.waves == k and p.threads == 64 * max(4, p.waves)
             if p.kind == _native.KIND_MFMA:
                 # one workgroup per tile over all of K: no split-K, nothing shared between workgroups
                 assert p.grid == p.tiles and p.splits == 1 and p.k_slice == k
@@ -200,23 +233,55 @@ def test_plan_kinds():
     _native.call("ftk_plan_project", 1, 4096, 4104, 0, 256, None, p)  # K % 512 != 0: the LDS-staged GEMV
     assert p.kind == _native.KIND_GEMV and p.threads == 256
     _native.call("ftk_plan_project", 4, 151936, 4096, _native.EPI_ARGMAX, 256, None, p)
+    assert p.kind == _native.KIND_QUAD and -(-p.tiles // p.grid) <= 8
+    _native.call("ftk_plan_project", 1, 151936, 4096, _native.EPI_ARGMAX, 256, None, p)
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
-    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # MFMA tiles on the STREAM schedule
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # 4x4x4 MFMA blocks on the STREAM schedule
+    assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.unroll == 4 and p.grid == 256
+    _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # with the norm
+    assert p.kind == _native.KIND_QUAD and p.rows_per_wave == 8 and p.waves == 8
+    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K at M <= 8
+    assert p.kind == _native.KIND_QUAD and p.waves == 8 and p.unroll == 12
+    _native.call("ftk_plan_project", 16, 4096, 4096, 0, 256, None, p)  # 16x16x32 MFMA tiles on the STREAM schedule
     assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 512 and p.unroll == 8
-    _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # small, with the norm
+    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # small, with the norm
     assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 1024 and p.unroll == 4
-    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K at M <= 8: the 8-row STREAM kernel
-    assert p.kind == _native.KIND_STREAM and p.waves == 8
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
     assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 16 and p.unroll == 2
     # K = 12288 with the prologue has no MFMA_STREAM kernel: the 8-row STREAM kernel (8 waves split K)
     _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
     assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
-    _native.call("ftk_plan_project", 5, 4096, 2048, 0, 256, None, p)  # neither STREAM kind has this K
+    _native.call("ftk_plan_project", 12, 4096, 2048, 0, 256, None, p)  # no STREAM-schedule kind has this K
     assert p.kind == _native.KIND_MFMA and p.grid == 256 and p.splits == 1
     _native.call("ftk_plan_project", 17, 4096, 4096, 0, 256, None, p)
     assert p.kind == _native.KIND_MFMA
     _native.call("ftk_plan_project", 20, 24576, 4096, _native.EPI_SWIGLU, 256, None, p)
     assert p.kind == _native.KIND_MFMA and p.rows_per_wave == 32 and p.grid == 12288 // 16
+
+
+def test_default_kind_for_8b_shapes():
+    """The planner's choice at the Qwen3-8B shapes (from the MI355X sweep): STREAM at M = 1 and,
+    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD at M = 5..8;
+    MFMA_STREAM at 9..16 (the 8-row STREAM kernel where K = 12288 has the prologue)."""
+    shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
+              "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
+              "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
+    for m in range(1, 17):
+        for name, (n, k, epi, pro) in shapes.items():
+            p = _native.Plan()
+            flags = epi | (_native.PLAN_PROLOGUE if pro else 0)
+            _native.call("ftk_plan_project", m, n, k, flags, 256, None, p)
+            quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
+            if m < quad_early:
+                want = _native.KIND_STREAM
+            elif m <= 8:
+                want = _native.KIND_QUAD
+            else:
+                want = _native.KIND_MFMA_STREAM
+            assert p.kind == want, (m, name, p.kind)
+    # the prologue at K = 12288 has no QUAD shape that fits the registers: the 8-row STREAM kernel
+    p = _native.Plan()
+    _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
