@@ -112,15 +112,14 @@ static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, i
 }
 
 // QUAD launch shape, from the M = 1..16 sweep of the Qwen3-8B shapes on MI355X:
-// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets)
-// and for lm_head from 5 rows, 8 otherwise; the first shape that fits the
-// registers (with the prologue at 9..16 rows, 4 rows per tile).
+// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets),
+// 8 otherwise; the first shape that fits the registers.
 struct QuadDefault {
   int rows, kw;
 };
 static QuadDefault quad_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
   if (M < 1 || M > kQuadMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
-  const int want = (epi == FTK_EPI_SWIGLU || (epi == FTK_EPI_ARGMAX && M > 4)) ? 16 : 8;
+  const int want = epi == FTK_EPI_SWIGLU ? 16 : 8;
   const QuadDefault order[] = {{want, 8}, {8, 8}, {4, 8}, {want, 4}, {8, 4}, {4, 4}, {8, 16}};
   for (const QuadDefault& d : order)
     if (quad_supported((int)M, d.rows, (int)K, d.kw, epi, pro)) return d;
@@ -131,9 +130,13 @@ static QuadDefault quad_default(int64_t M, int epi, bool pro, int64_t N, int64_t
 static int64_t quad_default_cap(int64_t M, int tiles, int cus) {
   return (tiles > 8192 && M <= 4) ? 32LL * cus : (int64_t)cus;
 }
-// Where QUAD beats STREAM below 5 rows (MI355X, Qwen3-8B shapes): lm_head from 2
-// rows, SwiGLU from 3, any projection with the prologue at 4.
+// Where QUAD beats the other kinds (MI355X, Qwen3-8B shapes): below 5 rows
+// (against STREAM) lm_head from 2 rows, SwiGLU from 3, any projection with the
+// prologue at 4; every projection at 5..8; at 9..16 (against MFMA_STREAM, whose
+// 16x16x32 tiles need a quarter of the MFMA issue per byte) the prologue
+// projection without an epilogue (QKV).
 static bool quad_preferred(int64_t M, int epi, bool pro) {
+  if (M > 8) return pro && epi == FTK_EPI_STORE;
   if (M >= 5) return true;
   if (epi == FTK_EPI_ARGMAX) return M >= 2;
   if (epi == FTK_EPI_SWIGLU) return M >= 3;
@@ -156,13 +159,13 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (epi == FTK_EPI_SWIGLU && (N % 2)) return FTK_ERR_INVALID;
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
   if (kind == FTK_KIND_AUTO) {
-    // Measured on MI355X at the Qwen3-8B shapes: STREAM (v_dot2) at M = 1 and,
-    // up to M = 4, where quad_preferred says so; QUAD (4x4x4 MFMA blocks) for
-    // M = 5..8; MFMA_STREAM (16x16x32) beyond.
+    // Measured on MI355X at the Qwen3-8B shapes: STREAM (v_dot2) at M = 1 and
+    // up to M = 4; QUAD (4x4x4 MFMA blocks) where quad_preferred says so;
+    // MFMA_STREAM (16x16x32) for the rest of M = 9..16.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     if (K % 8)
       kind = FTK_KIND_GENERIC;
-    else if (M <= 8 && quad && quad_preferred(M, epi, pro))
+    else if (quad && quad_preferred(M, epi, pro))
       kind = FTK_KIND_QUAD;
     else if (M <= 4 && stream_default(M, epi, N, K).rpw)
       kind = FTK_KIND_STREAM;

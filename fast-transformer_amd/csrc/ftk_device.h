@@ -68,17 +68,37 @@ __device__ __forceinline__ float dot8(u32x4_t w, u32x4_t x, float acc) {
   return acc;
 }
 
-// ss + the squares of 8 BF16 values, in element order. Every RMSNorm prologue
-// accumulates through this function, so all kernels scale a row identically.
+// ss + the squares of 8 BF16 values, a pair at a time (v_dot2_f32_bf16: the
+// squares are exact in FP32, accumulated in FP32). Every fused RMSNorm prologue
+// accumulates through this function, so the kinds that sum a row's chunks in
+// the same order scale it identically.
 __device__ __forceinline__ float sum_squares8(u32x4_t v, float ss) {
   const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lo = lo_f32(e[i]), hi = hi_f32(e[i]);
-    ss += lo * lo;
-    ss += hi * hi;
-  }
+  for (int i = 0; i < 4; ++i) ss = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(e[i]), as_bf16x2(e[i]), ss, false);
   return ss;
+}
+
+// The 8 BF16 values of a 16-byte chunk, widened exactly to FP32.
+__device__ __forceinline__ void widen8(u32x4_t v, float (&out)[8]) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = lo_f32(e[i]);
+    out[2 * i + 1] = hi_f32(e[i]);
+  }
+}
+
+// norm8 with the gain already widened (shared by the x rows of one K chunk).
+__device__ __forceinline__ u32x4_t norm8w(u32x4_t v, const float (&g)[8], float scale) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t n = rne_pair(lo_f32(e[i]) * scale, hi_f32(e[i]) * scale);
+    o[i] = rne_pair(lo_f32(n) * g[2 * i], hi_f32(n) * g[2 * i + 1]);
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
 }
 
 // RMSNorm of 8 BF16 values: bf16(bf16(x * scale) * gain), the cast order of

@@ -125,16 +125,22 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
     for (int j = 0; j < C; ++j) gv[j] = load16(a.gamma + first + j * kStep);
   }
 
-  // ---- first tile's weights in flight before the prologue ---------------------
+  // ---- the first tile's weight window: in flight during the prologue, except
+  // with 16 x rows and the prologue, whose raw rows, residual and gain would not
+  // fit in the registers beside it (then issued right after the prologue) ------
+  constexpr bool LATE = PRO && MQ >= 4;
   const int wg = blockIdx.x;  // tiles wg, wg + grid, ... (grid <= tiles)
   int tile = wg;
-  const uint16_t* wr[RS];
-  row_ptrs(tile, wr);
   u32x4_t wv[C][RS];
+  auto first_window = [&]() {
+    const uint16_t* wr[RS];
+    row_ptrs(tile, wr);
 #pragma unroll
-  for (int j = 0; j < C; ++j)
+    for (int j = 0; j < C; ++j)
 #pragma unroll
-    for (int r = 0; r < RS; ++r) wv[j][r] = load_stream16(wr[r] + j * kStep);
+      for (int r = 0; r < RS; ++r) wv[j][r] = load_stream16(wr[r] + j * kStep);
+  };
+  if constexpr (!LATE) first_window();
 
   // ---- RMSNorm prologue: normalise the slice in registers ---------------------
   if constexpr (PRO) {
@@ -158,16 +164,24 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
           for (int j = 0; j < C; ++j) store16(a.sum + (size_t)(4 * q + i4) * K + first + j * kStep, xr[q][j]);
     }
     __syncthreads();
+    float scale[MQ];
 #pragma unroll
     for (int q = 0; q < MQ; ++q) {
       float total = red[grp * KW][4 * q + i4];
 #pragma unroll
       for (int w = 1; w < KW; ++w) total += red[grp * KW + w][4 * q + i4];
-      const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
+      scale[q] = 1.0f / sqrtf(total / (float)K + a.eps);
+    }
+    // The gain of a chunk is widened once for the MQ rows that use it.
 #pragma unroll
-      for (int j = 0; j < C; ++j) xr[q][j] = norm8(xr[q][j], gv[j], scale);
+    for (int j = 0; j < C; ++j) {
+      float gf[8];
+      widen8(gv[j], gf);
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) xr[q][j] = norm8w(xr[q][j], gf, scale[q]);
     }
   }
+  if constexpr (LATE) first_window();
 
   // ---- tiles: consume, prefetch the next tile load by load, park the totals ----
   int count = 0;

@@ -116,3 +116,22 @@ def test_matches_mfma_kind_within_tolerance(cuda):
     a = L.rms_norm_linear(x, g, 1e-6, w, config=cfg(1, 16, 4))
     b = L.rms_norm_linear(x, g, 1e-6, w, config=_native.Config(_native.KIND_MFMA, 16, 4, 0, 16))
     assert within(to_bits(a), to_bits(b))
+
+
+@pytest.mark.parametrize("m", [5, 16])
+def test_residual_and_gathered_rows(cuda, m):
+    """The prologue's residual add and embedding gather on this kind, the stored sum bit-exact."""
+    k, n = 4096, 1500
+    x, w, g = _inputs(m, n, k, seed=1400 + m, device=cuda)
+    r = seeded((m, k), seed=1410 + m, device=cuda)
+    c = cfg(1, 16, 4)
+    y, summed = L.add_rms_norm_linear(x, r, g, 1e-6, w, config=c)
+    want_y, want_sum = path.add_norm_project(to_bits(x), to_bits(r), to_bits(g), 1e-6, to_bits(w))
+    np.testing.assert_array_equal(to_bits(summed), want_sum)
+    assert within(to_bits(y), want_y)
+    table = seeded((64, k), seed=1420 + m, device=cuda)
+    ids = torch.tensor([(5 * i + 1) % 64 for i in range(m)], device=cuda, dtype=torch.int32)
+    y2, hidden = L.embed_rms_norm_linear(ids, table, g, 1e-6, w, config=c)
+    rows = to_bits(table)[ids.cpu().numpy()]
+    np.testing.assert_array_equal(to_bits(hidden), rows)
+    assert within(to_bits(y2), path.norm_project(rows, to_bits(g), 1e-6, to_bits(w)))

@@ -46,8 +46,8 @@ def _inputs(m, n, k, seed, device):
 CASES = [
     (1, 1536, 4096, _native.KIND_STREAM), (3, 1000, 4096, _native.KIND_STREAM),
     (4, 777, 1024, _native.KIND_QUAD), (2, 500, 12288, _native.KIND_STREAM),
-    (5, 1500, 4096, _native.KIND_QUAD), (16, 2000, 4096, _native.KIND_MFMA_STREAM),
-    (7, 900, 12288, _native.KIND_STREAM), (12, 1200, 4096, _native.KIND_MFMA_STREAM),
+    (5, 1500, 4096, _native.KIND_QUAD), (16, 2000, 4096, _native.KIND_QUAD),
+    (7, 900, 12288, _native.KIND_STREAM), (12, 1200, 4096, _native.KIND_QUAD),
     (2, 700, 1000, _native.KIND_GEMV), (6, 700, 1000, _native.KIND_MFMA), (20, 640, 4096, _native.KIND_MFMA),
 ]
 

@@ -134,7 +134,9 @@ QUAD_ONE = ((1, 8, 4), (1, 4, 8), (1, 12, 8))
 
 def _quad_fits(mq, rs, c, kw, pro):
     """The register estimate of the QUAD kind (x slice, weight window, accumulators, prologue inputs)."""
-    est = 4 * mq * c + 4 * rs * c + 4 * rs * mq + (6 * mq * c + 4 * c if pro else 0) + 32
+    main_loop = 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32
+    prologue = 10 * mq * c + 4 * c + 32  # 16 x rows: the window waits for the prologue
+    est = main_loop if not pro else max(main_loop, prologue) if mq >= 4 else main_loop + 6 * mq * c + 4 * c
     return est <= (128 if kw >= 16 else 248)
 
 
@@ -246,8 +248,8 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_QUAD and p.waves == 8 and p.unroll == 12
     _native.call("ftk_plan_project", 16, 4096, 4096, 0, 256, None, p)  # 16x16x32 MFMA tiles on the STREAM schedule
     assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 512 and p.unroll == 8
-    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # small, with the norm
-    assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 1024 and p.unroll == 4
+    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # QKV: 4x4x4 blocks
+    assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.rows_per_wave == 8
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
     assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 16 and p.unroll == 2
     # K = 12288 with the prologue has no MFMA_STREAM kernel: the 8-row STREAM kernel (8 waves split K)
@@ -263,8 +265,9 @@ def test_plan_kinds():
 
 def test_default_kind_for_8b_shapes():
     """The planner's choice at the Qwen3-8B shapes (from the MI355X sweep): STREAM at M = 1 and,
-    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD at M = 5..8;
-    MFMA_STREAM at 9..16 (the 8-row STREAM kernel where K = 12288 has the prologue)."""
+    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD at M = 5..8
+    and for QKV to 16; MFMA_STREAM for the rest of 9..16 (the 8-row STREAM kernel where
+    K = 12288 has the prologue)."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -276,7 +279,7 @@ def test_default_kind_for_8b_shapes():
             quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
             if m < quad_early:
                 want = _native.KIND_STREAM
-            elif m <= 8:
+            elif m <= 8 or name == "qkv":
                 want = _native.KIND_QUAD
             else:
                 want = _native.KIND_MFMA_STREAM
