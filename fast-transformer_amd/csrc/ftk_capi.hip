@@ -112,14 +112,15 @@ static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, i
 }
 
 // QUAD launch shape, from the M = 1..16 sweep of the Qwen3-8B shapes on MI355X:
-// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets),
-// 8 otherwise; the first shape that fits the registers.
+// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets)
+// and for lm_head at up to 4 rows, 24 for a projection with the prologue at up
+// to 4 rows (QKV), 8 otherwise; the first shape that fits the registers.
 struct QuadDefault {
   int rows, kw;
 };
 static QuadDefault quad_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
   if (M < 1 || M > kQuadMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
-  const int want = epi == FTK_EPI_SWIGLU ? 16 : 8;
+  const int want = (epi == FTK_EPI_SWIGLU || (epi == FTK_EPI_ARGMAX && M <= 4)) ? 16 : (pro && M <= 4) ? 24 : 8;
   const QuadDefault order[] = {{want, 8}, {8, 8}, {4, 8}, {want, 4}, {8, 4}, {4, 4}, {8, 16}};
   for (const QuadDefault& d : order)
     if (quad_supported((int)M, d.rows, (int)K, d.kw, epi, pro)) return d;

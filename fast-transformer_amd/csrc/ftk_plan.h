@@ -124,16 +124,23 @@ FTK_HD int quad_groups(int m) { return m < 1 ? 0 : m <= 4 ? 1 : m <= 8 ? 2 : m <
 // gfx950 builds: the x slice (4 MQ C), the weight window (4 RS C), the
 // accumulators (4 RS MQ) and, with the prologue, what is live while it runs:
 // the residual, the gain and the normalisation's temporaries (6 MQ C + 4 C).
-// With 16 x rows and the prologue the window is issued after the prologue, so
-// the two peaks do not add. The cap is 248 registers (128 for a 16-wave
-// workgroup); shapes over it are not built.
+// Where both would not fit, the window is issued after the prologue, so the two
+// peaks do not add. The cap is 248 registers (128 for a 16-wave workgroup);
+// shapes over it are not built.
+constexpr int quad_cap(int kw) { return kw >= 16 ? 128 : 248; }
+constexpr int quad_main_regs(int mq, int rs, int c) { return 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32; }
+// With the prologue: issue the first weight window only after it, where the two
+// would not fit together.
+constexpr bool quad_late(int mq, int rs, int c, int kw, bool pro) {
+  return pro && quad_main_regs(mq, rs, c) + 6 * mq * c + 4 * c > quad_cap(kw);
+}
 constexpr bool quad_fits(int mq, int rs, int c, int kw, bool pro) {
-  const int cap = kw >= 16 ? 128 : 248;
-  const int main_loop = 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32;
-  const int prologue = 4 * mq * c + 6 * mq * c + 4 * c + 32;
-  const int est = !pro ? main_loop : mq >= 4 ? (main_loop > prologue ? main_loop : prologue)
-                                             : main_loop + 6 * mq * c + 4 * c;
-  return est <= cap;
+  const int main_loop = quad_main_regs(mq, rs, c);
+  const int prologue = 10 * mq * c + 4 * c + 32;
+  const int est = !pro ? main_loop
+                       : quad_late(mq, rs, c, kw, pro) ? (main_loop > prologue ? main_loop : prologue)
+                                                       : main_loop + 6 * mq * c + 4 * c;
+  return est <= quad_cap(kw);
 }
 
 // ---- workspace layout of one projection call (bytes) -----------------------

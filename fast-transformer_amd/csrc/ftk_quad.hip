@@ -126,9 +126,9 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
   }
 
   // ---- the first tile's weight window: in flight during the prologue, except
-  // with 16 x rows and the prologue, whose raw rows, residual and gain would not
-  // fit in the registers beside it (then issued right after the prologue) ------
-  constexpr bool LATE = PRO && MQ >= 4;
+  // where the prologue's raw rows, residual and gain would not fit in the
+  // registers beside it (then issued right after the prologue) -----------------
+  constexpr bool LATE = quad_late(MQ, RS, C, KW, PRO);
   const int wg = blockIdx.x;  // tiles wg, wg + grid, ... (grid <= tiles)
   int tile = wg;
   u32x4_t wv[C][RS];
@@ -282,13 +282,14 @@ typedef void (*QuadKernel)(ProjArgs, int);
 
 // Instantiated (row sets RS, segments per lane C, KW), where they fit the
 // registers (quad_fits): K = 4096 (the 8B model's QKV, O, gate/up, lm_head)
-// with 4 or 8 waves splitting K; K = 12288 (down) with 8 or 16; K = 1024 /
-// 2048 / 3072 (the 0.6B model) with 4.
+// with 4 or 8 waves splitting K and up to 24 rows per tile; K = 12288 (down)
+// with 8 or 16; K = 1024 / 2048 / 3072 (the 0.6B model) with 4.
 #define FTK_QUAD_SHAPES(MQ, PRO, EPI)   \
   FTK_QUAD_SHAPE(MQ, 2, 8, 4, PRO, EPI)  \
   FTK_QUAD_SHAPE(MQ, 4, 8, 4, PRO, EPI)  \
   FTK_QUAD_SHAPE(MQ, 2, 4, 8, PRO, EPI)  \
   FTK_QUAD_SHAPE(MQ, 4, 4, 8, PRO, EPI)  \
+  FTK_QUAD_SHAPE(MQ, 6, 4, 8, PRO, EPI)  \
   FTK_QUAD_SHAPE(MQ, 2, 12, 8, PRO, EPI) \
   FTK_QUAD_SHAPE(MQ, 2, 6, 16, PRO, EPI) \
   FTK_QUAD_SHAPE(MQ, 2, 2, 4, PRO, EPI)  \

@@ -26,8 +26,8 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-2, 1e-2
 
 #: (rows per group, K, KW) launch shapes, each built for the row counts whose registers fit.
-SHAPES = ((8, 4096, 4), (16, 4096, 4), (8, 4096, 8), (16, 4096, 8), (8, 12288, 8), (8, 12288, 16), (8, 1024, 4),
-          (8, 2048, 4), (8, 3072, 4), (4, 4096, 4), (4, 4096, 8), (4, 12288, 8))
+SHAPES = ((8, 4096, 4), (16, 4096, 4), (8, 4096, 8), (16, 4096, 8), (24, 4096, 8), (8, 12288, 8),
+          (8, 12288, 16), (8, 1024, 4), (8, 2048, 4), (8, 3072, 4), (4, 4096, 4), (4, 4096, 8), (4, 12288, 8))
 
 
 def within(got_bits, want_bits):

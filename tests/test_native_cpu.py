@@ -128,16 +128,19 @@ def _mstream_status(m, k, epilogue, t, kw, u):
 
 #: (row sets RS, segments per lane C, KW) the QUAD kind may build (K = 128 C KW); single row sets
 #: only for store / argmax. A shape is built for a row count only where it fits the registers.
-QUAD_SHAPES = ((2, 8, 4), (4, 8, 4), (2, 4, 8), (4, 4, 8), (2, 12, 8), (2, 6, 16), (2, 2, 4), (2, 4, 4), (2, 6, 4))
+QUAD_SHAPES = ((2, 8, 4), (4, 8, 4), (2, 4, 8), (4, 4, 8), (6, 4, 8), (2, 12, 8), (2, 6, 16), (2, 2, 4), (2, 4, 4),
+               (2, 6, 4))
 QUAD_ONE = ((1, 8, 4), (1, 4, 8), (1, 12, 8))
 
 
 def _quad_fits(mq, rs, c, kw, pro):
     """The register estimate of the QUAD kind (x slice, weight window, accumulators, prologue inputs)."""
+    cap = 128 if kw >= 16 else 248
     main_loop = 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32
-    prologue = 10 * mq * c + 4 * c + 32  # 16 x rows: the window waits for the prologue
-    est = main_loop if not pro else max(main_loop, prologue) if mq >= 4 else main_loop + 6 * mq * c + 4 * c
-    return est <= (128 if kw >= 16 else 248)
+    prologue = 10 * mq * c + 4 * c + 32
+    late = pro and main_loop + 6 * mq * c + 4 * c > cap  # the window waits for the prologue
+    est = main_loop if not pro else max(main_loop, prologue) if late else main_loop + 6 * mq * c + 4 * c
+    return est <= cap
 
 
 def _quad_status(m, k, epilogue, rows, kw, pro=False):
