@@ -95,7 +95,8 @@ static int64_t stream_default_cap(int tiles, int cus) {
 // MI355X: 8 waves split K (16 steps of 32 at K = 4096) with 8 steps in flight
 // (16 for lm_head); 16 waves and 4 steps for a small projection with the
 // prologue (QKV); two subtiles per tile for SwiGLU (a gate and an up subtile).
-// K = 12288 has only the 16-wave kernel (24 steps), without the prologue.
+// K = 12288 runs without the prologue only, with x streamed: 8 waves, 16 steps
+// in flight.
 struct MstreamDefault {
   int t, kw, unroll;
 };
@@ -103,9 +104,12 @@ static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, i
   if (M < 1 || M > kMstreamMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
   const int t = epi == FTK_EPI_SWIGLU ? 2 : 1;
   const bool small_pro = pro && epi == FTK_EPI_STORE && mfma_tiles(epi, (int)N, 1) <= 512;
+  // Long K without the prologue streams x beside the weights: 16 steps in flight.
+  const bool long_k = !pro && mstream_steps((int)K, 8) > 16;
   const MstreamDefault order[] = {
-      small_pro ? MstreamDefault{t, 16, 4} : MstreamDefault{t, 8, epi == FTK_EPI_ARGMAX ? 16 : 8},
-      {t, 8, 8}, {t, 8, 4}, {t, 16, 4}, {t, 16, 2}};
+      long_k ? MstreamDefault{t, 8, 16}
+             : small_pro ? MstreamDefault{t, 16, 4} : MstreamDefault{t, 8, epi == FTK_EPI_ARGMAX ? 16 : 8},
+      {t, 8, 8}, {t, 8, 4}, {t, 16, 4}, {t, 16, 6}, {t, 16, 2}};
   for (const MstreamDefault& d : order)
     if (mstream_supported((int)M, d.t, (int)K, d.kw, d.unroll, epi, pro)) return d;
   return {0, 0, 0};

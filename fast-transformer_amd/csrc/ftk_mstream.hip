@@ -14,6 +14,9 @@
 //   * Lane l only ever needs x at its own k, so its S steps of x are loaded once
 //     into registers (and normalised there when the prologue is on: one
 //     barrier to combine the row sums of squares), never re-read per tile.
+//     For the long K without the prologue (K = 12288) x instead streams beside
+//     the weights with the same lookahead (L2 hits), which leaves the registers
+//     to a deeper weight window; the sums are the same either way.
 //   * Rolling window: the weight loads of the next U steps are in flight at all
 //     times, across tile boundaries (step s of tile i is consumed, then step
 //     s + U, possibly of tile i + 1, is loaded into the registers it freed).
@@ -43,13 +46,21 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
   // throughput than interleaving the waves' steps).
   auto koff = [&](int s) { return (size_t)(32 * (kw * S + s) + 8 * g); };
 
-  // ---- x slice first, then the first weight window ----------------------------
-  // With the prologue, row li is x[li] or the gathered x[x_ids[li]], plus the residual.
-  const uint16_t* xrow = (PRO && mine) ? x_row(a, li) : a.x + (size_t)li * K;
-  u32x4_t xr[S];
+  // The x slice: with the prologue (row li is x[li] or the gathered x[x_ids[li]],
+  // plus the residual) and for K up to 16 steps per wave, all S steps stay in
+  // registers. For the long K without the prologue (XS) a resident slice would
+  // leave no registers for the weight window, so x streams beside the weights:
+  // step s's x is loaded with step s's weights (waiting for one never waits for
+  // later-issued loads) and hits in L2. The sums are the same either way.
+  constexpr bool XS = !PRO && S > 16;
+  const uint16_t* xrow = (PRO && mine) ? x_row(a, li) : a.x + (size_t)(mine ? li : 0) * K;
+  auto x_step = [&](int s) { return mine ? load16(xrow + koff(s)) : u32x4_t{0u, 0u, 0u, 0u}; };
+  u32x4_t xr[XS ? 1 : S];
+  u32x4_t xv[XS ? U : 1];
+  if constexpr (!XS) {
 #pragma unroll
-  for (int s = 0; s < S; ++s)
-    xr[s] = !mine ? u32x4_t{0u, 0u, 0u, 0u} : PRO ? prologue_in(a, xrow, li, koff(s)) : load16(xrow + koff(s));
+    for (int s = 0; s < S; ++s) xr[s] = !mine ? u32x4_t{0u, 0u, 0u, 0u} : PRO ? prologue_in(a, xrow, li, koff(s)) : x_step(s);
+  }
 
   const int wg = blockIdx.x;
   int tile = wg;  // grid <= tiles
@@ -61,9 +72,11 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
   rows_of(tile, wp);
   u32x4_t wv[U][T];
 #pragma unroll
-  for (int q = 0; q < U; ++q)
+  for (int q = 0; q < U; ++q) {
 #pragma unroll
     for (int t = 0; t < T; ++t) wv[q][t] = load_stream16(wp[t] + koff(q));
+    if constexpr (XS) xv[q] = x_step(q);
+  }
 
   // ---- RMSNorm prologue: row sums of squares over (wave, group, step) in order
   if constexpr (PRO) {
@@ -84,7 +97,8 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
     for (int w = 1; w < KW; ++w) total += red[w][li];
     const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
     // The gain is loaded only now (cache hits behind the weight window), so its
-    // S registers are never live beside the window's.
+    // S registers are never live beside the window's (measured faster here than
+    // loading it before the window).
 #pragma unroll
     for (int s = 0; s < S; ++s) xr[s] = norm8(xr[s], load16(a.gamma + koff(s)), scale);
   }
@@ -101,15 +115,18 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
     for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < S; ++s) {
+      const u32x4_t xs = XS ? xv[s % U] : xr[XS ? 0 : s];
 #pragma unroll
-      for (int t = 0; t < T; ++t) acc[t] = mfma16x16x32(wv[s % U][t], xr[s], acc[t]);
+      for (int t = 0; t < T; ++t) acc[t] = mfma16x16x32(wv[s % U][t], xs, acc[t]);
       // refill the freed window slot: step s + U of this tile, or of the next
       if (s + U < S) {
 #pragma unroll
         for (int t = 0; t < T; ++t) wv[s % U][t] = load_stream16(wp[t] + koff(s + U));
+        if constexpr (XS) xv[s % U] = x_step(s + U);
       } else if (more) {
 #pragma unroll
         for (int t = 0; t < T; ++t) wv[s % U][t] = load_stream16(wn[t] + koff(s + U - S));
+        if constexpr (XS) xv[s % U] = x_step(s + U - S);
       }
     }
 #pragma unroll
@@ -186,7 +203,8 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
 typedef void (*MstreamKernel)(ProjArgs, int);
 
 // Instantiated (T, S, KW, U): K = 4096 (S = 8 at KW = 16, S = 16 at KW = 8) and,
-// without the prologue (the 8B down projection), K = 12288 (S = 24 at KW = 16).
+// without the prologue (x streamed), deeper windows and K = 12288 (S = 24 at
+// KW = 16, S = 48 at KW = 8; the 8B down projection).
 #define FTK_MSTREAM_SHAPES_EVEN(PRO, EPI)  \
   FTK_MSTREAM_SHAPE(2, 8, 16, 4, PRO, EPI) \
   FTK_MSTREAM_SHAPE(2, 16, 8, 4, PRO, EPI) \
@@ -199,7 +217,10 @@ typedef void (*MstreamKernel)(ProjArgs, int);
   FTK_MSTREAM_SHAPE(1, 16, 8, 8, PRO, EPI) \
   FTK_MSTREAM_SHAPE(1, 16, 8, 16, PRO, EPI)
 
-#define FTK_MSTREAM_SHAPES_LONG(EPI) FTK_MSTREAM_SHAPE(1, 24, 16, 2, false, EPI)
+#define FTK_MSTREAM_SHAPES_LONG(EPI)         \
+  FTK_MSTREAM_SHAPE(1, 24, 16, 2, false, EPI) \
+  FTK_MSTREAM_SHAPE(1, 24, 16, 6, false, EPI) \
+  FTK_MSTREAM_SHAPE(1, 48, 8, 16, false, EPI)
 
 #define FTK_MSTREAM_SHAPE(T_, S_, KW_, U_, PRO, EPI) \
   if (t == T_ && s == S_ && kw == KW_ && u == U_) return mstream_kernel<T_, S_, KW_, U_, PRO, EPI>;

@@ -28,8 +28,8 @@ ATOL, RTOL = 2e-2, 1e-2
 SHAPES_EVEN = ((2, 4096, 16, 4), (2, 4096, 8, 4), (2, 4096, 8, 8))
 #: ... for store / argmax only ...
 SHAPES_ONE = ((1, 4096, 16, 4), (1, 4096, 16, 8), (1, 4096, 8, 4), (1, 4096, 8, 8), (1, 4096, 8, 16))
-#: ... and without the prologue only.
-SHAPES_NO_PROLOGUE = ((2, 4096, 16, 8), (2, 4096, 8, 16), (1, 12288, 16, 2))
+#: ... and without the prologue only (x streamed beside the weights).
+SHAPES_NO_PROLOGUE = ((2, 4096, 16, 8), (2, 4096, 8, 16), (1, 12288, 16, 2), (1, 12288, 16, 6), (1, 12288, 8, 16))
 
 
 def within(got_bits, want_bits):
@@ -135,3 +135,18 @@ def test_residual_and_gathered_rows(cuda, m):
     rows = to_bits(table)[ids.cpu().numpy()]
     np.testing.assert_array_equal(to_bits(hidden), rows)
     assert within(to_bits(y2), path.norm_project(rows, to_bits(g), 1e-6, to_bits(w)))
+
+
+@pytest.mark.parametrize("u", [4, 8, 16])
+def test_streamed_x_window_does_not_change_bits(cuda, u):
+    """Without the prologue x streams beside the weights with the window's lookahead: the window
+    depth only moves loads, so every depth gives the same bits (and the oracle's values)."""
+    x, w, _ = _inputs(13, 3000, 4096, seed=1500 + u, device=cuda)
+    streamed = L.project(x, w, cfg(1, 8, u))
+    assert within(to_bits(streamed), path.project(to_bits(x), to_bits(w)))
+    assert torch.equal(streamed, L.project(x, w, cfg(1, 8, 4)))
+    k = 12288  # the long-K shapes exist only with x streamed
+    x2, w2, _ = _inputs(16, 1000, k, seed=1510 + u, device=cuda)
+    a = L.project(x2, w2, cfg(1, 8, 16))
+    assert within(to_bits(a), path.project(to_bits(x2), to_bits(w2)))
+    assert within(to_bits(L.project(x2, w2, cfg(1, 16, 6))), to_bits(a))

@@ -113,7 +113,8 @@ def _stream_status(m, k, rpw, kw):
 
 #: (T, S, KW, U) the MFMA_STREAM kind instantiates (K = 32 S KW), by epilogue, without the prologue.
 MSTREAM_EVEN = ((2, 8, 16, 4), (2, 16, 8, 4), (2, 16, 8, 8), (2, 16, 8, 16), (2, 8, 16, 8))
-MSTREAM_ONE = ((1, 8, 16, 4), (1, 8, 16, 8), (1, 16, 8, 4), (1, 16, 8, 8), (1, 16, 8, 16), (1, 24, 16, 2))
+MSTREAM_ONE = ((1, 8, 16, 4), (1, 8, 16, 8), (1, 16, 8, 4), (1, 16, 8, 8), (1, 16, 8, 16), (1, 24, 16, 2),
+               (1, 24, 16, 6), (1, 48, 8, 16))
 
 
 def _mstream_shapes(epilogue):
@@ -253,8 +254,8 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 512 and p.unroll == 8
     _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # QKV: 4x4x4 blocks
     assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.rows_per_wave == 8
-    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
-    assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 16 and p.unroll == 2
+    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # x streamed beside the weights
+    assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 8 and p.unroll == 16
     # K = 12288 with the prologue has no MFMA_STREAM kernel: the 8-row STREAM kernel (8 waves split K)
     _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
     assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
