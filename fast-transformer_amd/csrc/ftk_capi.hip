@@ -137,15 +137,31 @@ static int64_t quad_default_cap(int64_t M, int tiles, int cus) {
 }
 // Where QUAD beats the other kinds (MI355X, Qwen3-8B shapes): below 5 rows
 // (against STREAM) lm_head from 2 rows, SwiGLU from 3, any projection with the
-// prologue at 4; every projection at 5..8; at 9..16 (against MFMA_STREAM, whose
-// 16x16x32 tiles need a quarter of the MFMA issue per byte) the prologue
-// projection without an epilogue (QKV).
+// prologue at 4; at 5..8 (against STAGE) the fused projections (prologue,
+// SwiGLU or argmax). From 9 rows STAGE's 16x16x32 tiles, a quarter of the MFMA
+// issue per byte, win everywhere.
 static bool quad_preferred(int64_t M, int epi, bool pro) {
-  if (M > 8) return pro && epi == FTK_EPI_STORE;
-  if (M >= 5) return true;
+  if (M > 8) return false;
+  if (M >= 5) return pro || epi != FTK_EPI_STORE;
   if (epi == FTK_EPI_ARGMAX) return M >= 2;
   if (epi == FTK_EPI_SWIGLU) return M >= 3;
   return pro && M >= 4;
+}
+
+// STAGE launch shape, from the M = 5..16 sweep of the Qwen3-8B shapes on MI355X:
+// 8 waves split K; two segments in flight (three for the long K, four for
+// lm_head); two subtiles per tile for SwiGLU (a gate and an up subtile).
+struct StageDefault {
+  int t, kw, unroll;
+};
+static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
+  if (M < 1 || M > kStageMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
+  const int t = epi == FTK_EPI_SWIGLU ? 2 : 1;
+  const int u = quad_segments((int)K, 8) > 4 ? 3 : epi == FTK_EPI_ARGMAX ? 4 : 2;
+  const StageDefault order[] = {{t, 8, u}, {t, 8, 2}, {t, 8, 4}, {t, 8, 3}};
+  for (const StageDefault& d : order)
+    if (stage_supported((int)M, d.t, (int)K, d.kw, d.unroll, epi, pro)) return d;
+  return {0, 0, 0};
 }
 
 constexpr int kMfmaDefaultUnroll = 4;
@@ -165,13 +181,17 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
   if (kind == FTK_KIND_AUTO) {
     // Measured on MI355X at the Qwen3-8B shapes: STREAM (v_dot2) at M = 1 and
-    // up to M = 4; QUAD (4x4x4 MFMA blocks) where quad_preferred says so;
-    // MFMA_STREAM (16x16x32) for the rest of M = 9..16.
+    // up to M = 4; QUAD (4x4x4 MFMA blocks) where quad_preferred says so; STAGE
+    // (16x16x32 via LDS) for the rest of M = 5..16; MFMA_STREAM where neither has
+    // the shape.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
+    const bool stage = M >= 5 && stage_default(M, epi, pro, N, K).t != 0;
     if (K % 8)
       kind = FTK_KIND_GENERIC;
     else if (quad && quad_preferred(M, epi, pro))
       kind = FTK_KIND_QUAD;
+    else if (stage)
+      kind = FTK_KIND_STAGE;
     else if (M <= 4 && stream_default(M, epi, N, K).rpw)
       kind = FTK_KIND_STREAM;
     else if (M <= 4)
@@ -262,6 +282,28 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
                                                   : quad_default_cap(M, p->tiles, cus);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
+    const int64_t units = cap > floor ? cap : floor;
+    p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
+    return FTK_OK;
+  }
+  if (kind == FTK_KIND_STAGE) {
+    if (M > kStageMaxRows) return FTK_ERR_UNSUPPORTED;
+    const StageDefault d = stage_default(M, epi, pro, N, K);
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 16 * (d.t ? d.t : 1);
+    const int kw = cfg && cfg->waves ? cfg->waves : (d.kw ? d.kw : 8);
+    const int unroll = cfg && cfg->unroll ? cfg->unroll : (d.unroll ? d.unroll : 2);
+    if (quad_segments((int)K, kw) == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
+    if (rows % 16 || !stage_supported((int)M, rows / 16, (int)K, kw, unroll, epi, pro)) return FTK_ERR_INVALID;
+    const int t = rows / 16;
+    p->rows_per_wave = rows;
+    p->unroll = unroll;
+    p->waves = kw;
+    p->threads = 64 * kw;
+    p->tiles = mfma_tiles(epi, (int)N, t);
+    const int64_t cap = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
+    const int depth = stage_max_depth(t, kw);
+    const int64_t floor = (p->tiles + depth - 1) / depth;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
@@ -396,11 +438,12 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
     }
     return FTK_OK;
   }
-  if (p->kind == FTK_KIND_MFMA_STREAM) {
+  if (p->kind == FTK_KIND_MFMA_STREAM || p->kind == FTK_KIND_STAGE) {
     // Workgroup b walks tiles b + i grid; a tile is T subtiles of 16 weight rows.
     const int t = p->rows_per_wave / 16;
     if (t < 1 || p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
-    if ((p->tiles + p->grid - 1) / p->grid > mstream_max_depth(t, p->waves)) return FTK_ERR_INVALID;
+    const int depth = p->kind == FTK_KIND_STAGE ? stage_max_depth(t, p->waves) : mstream_max_depth(t, p->waves);
+    if ((p->tiles + p->grid - 1) / p->grid > depth) return FTK_ERR_INVALID;
     const int per = mfma_out_per_tile(epilogue, t);
     for (int b = 0; b < p->grid; ++b)
       for (int tile = b; tile < p->tiles; tile += p->grid) {
@@ -514,6 +557,9 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
   } else if (p.kind == FTK_KIND_QUAD) {
     QuadShape g = {p.rows_per_wave, p.waves, p.grid, p.tiles};
     e = launch_quad(a, epilogue, g, s);
+  } else if (p.kind == FTK_KIND_STAGE) {
+    StageShape g = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid, p.tiles};
+    e = launch_stage(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);

@@ -99,6 +99,17 @@ struct QuadShape {
 bool quad_supported(int M, int rows, int K, int kw, int epi, bool pro);
 hipError_t launch_quad(const ProjArgs& a, int epi, const QuadShape& shape, hipStream_t stream);
 
+// Launch shape of the STAGE kind (K = 128 C KW; weights staged through LDS into 16x16x32 MFMAs).
+struct StageShape {
+  int subtiles;  // T: 16-row MFMA subtiles per tile
+  int unroll;    // U: K segments of weight loads in flight per wave
+  int kw;        // waves per workgroup, splitting K
+  int grid;      // workgroups; each walks <= stage_max_depth(T, KW) tiles
+  int tiles;
+};
+bool stage_supported(int M, int t, int K, int kw, int unroll, int epi, bool pro);
+hipError_t launch_stage(const ProjArgs& a, int epi, const StageShape& shape, hipStream_t stream);
+
 // Launch shape of the MFMA kind.
 struct MfmaShape {
   int subtiles;  // T: 16-row MFMA subtiles per workgroup

@@ -17,7 +17,7 @@ LIB_PATH = Path(__file__).with_name("libftk.so")
 FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = range(5)
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
 PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
-KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD = range(7)
+KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE = range(8)
 MAX_ROWS = 32
 
 _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float

@@ -63,8 +63,10 @@ typedef enum ftk_kind {
   FTK_KIND_STREAM = 4,   /* M <= 8, K = 512 C KW: HBM-streaming GEMV, x slice in registers,
                             rolling weight prefetch, one barrier per workgroup */
   FTK_KIND_MFMA_STREAM = 5, /* M <= 16, K = 32 S KW: the STREAM schedule on 16x16x32 MFMA tiles */
-  FTK_KIND_QUAD = 6         /* M <= 16, K = 128 C KW: the STREAM schedule on 16-block 4x4x4 MFMAs,
+  FTK_KIND_QUAD = 6,        /* M <= 16, K = 128 C KW: the STREAM schedule on 16-block 4x4x4 MFMAs,
                                weights loaded as 4 rows x 256 contiguous bytes per wave load */
+  FTK_KIND_STAGE = 7        /* M <= 16, K = 128 C KW: QUAD's weight loads staged through LDS into
+                               16x16x32 MFMA tiles */
 } ftk_kind;
 
 /* Launch choice for one projection (the reference's per-shape config tuple,
@@ -73,16 +75,18 @@ typedef enum ftk_kind {
 typedef struct ftk_config {
   int kind;            /* ftk_kind */
   int rows_per_wave;   /* GEMV, STREAM: weight rows per row group per tile (1..8);
-                          MFMA: rows per workgroup (16, 32, 64); MFMA_STREAM: rows per tile (16, 32);
-                          QUAD: weight rows per row group per tile (4, 8, 16; SwiGLU 8, 16) */
+                          MFMA: rows per workgroup (16, 32, 64); MFMA_STREAM, STAGE: rows per tile
+                          (16, 32); QUAD: weight rows per row group per tile (4, 8, 16, 24; SwiGLU
+                          8, 16, 24) */
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
                           MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4);
                           STREAM, QUAD: unused (K fixes the chunks per lane);
-                          MFMA_STREAM: K steps of weight loads in flight per wave (2, 4, 8) */
-  int groups_per_cu;   /* GEMV, STREAM, MFMA_STREAM, QUAD: grid cap = groups_per_cu * CUs (grid-stride
+                          MFMA_STREAM: K steps of weight loads in flight per wave (2, 4, 8);
+                          STAGE: 128-wide K segments of weight loads in flight per wave (2..6) */
+  int groups_per_cu;   /* GEMV, STREAM, MFMA_STREAM, QUAD, STAGE: grid cap = groups_per_cu * CUs (grid-stride
                           beyond; the STREAM kinds raise the grid so no workgroup walks more tiles
                           than its LDS holds); MFMA: unused */
-  int waves;           /* MFMA, MFMA_STREAM: waves per workgroup splitting K (4, 8, 16);
+  int waves;           /* MFMA, MFMA_STREAM, STAGE: waves per workgroup splitting K (4, 8, 16);
                           GEMV, STREAM: waves per row group splitting K (1, 2, 4, 8; a workgroup is
                           4 waves, or 8 when 8 split K);
                           QUAD: waves per row group splitting K (4, 8, 16; the workgroup is

@@ -5,10 +5,10 @@ The fused calls must give what the reference's separate launches give
 projection): projections within |y - ref| <= 2e-2 + 1e-2|ref| of the CPU
 oracle, greedy ids bit-exact, and the stored residual stream (x + residual,
 or the gathered embedding rows) bit for bit: it is a BF16 add or a copy.
-Every kind that has the fused form is covered: STREAM (M <= 8), QUAD (M <= 16),
-MFMA_STREAM (M <= 16), the LDS-staged GEMV (K not 512 C KW), the MFMA kind (its
-row-scale pre-pass stores the rows), and shapes with no fused form fall back to
-the separate kernels with the same results.
+Every kind that has the fused form is covered: STREAM (M <= 8), QUAD and STAGE
+(M <= 16; MFMA_STREAM in its own file), the LDS-staged GEMV (K not 512 C KW), the
+MFMA kind (its row-scale pre-pass stores the rows), and shapes with no fused
+form fall back to the separate kernels with the same results.
 """
 
 import numpy as np
@@ -46,8 +46,8 @@ def _inputs(m, n, k, seed, device):
 CASES = [
     (1, 1536, 4096, _native.KIND_STREAM), (3, 1000, 4096, _native.KIND_STREAM),
     (4, 777, 1024, _native.KIND_QUAD), (2, 500, 12288, _native.KIND_STREAM),
-    (5, 1500, 4096, _native.KIND_QUAD), (16, 2000, 4096, _native.KIND_QUAD),
-    (7, 900, 12288, _native.KIND_STREAM), (12, 1200, 4096, _native.KIND_QUAD),
+    (5, 1500, 4096, _native.KIND_QUAD), (16, 2000, 4096, _native.KIND_STAGE),
+    (7, 900, 12288, _native.KIND_STREAM), (12, 1200, 4096, _native.KIND_STAGE),
     (2, 700, 1000, _native.KIND_GEMV), (6, 700, 1000, _native.KIND_MFMA), (20, 640, 4096, _native.KIND_MFMA),
 ]
 

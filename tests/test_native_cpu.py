@@ -154,6 +154,20 @@ def _quad_status(m, k, epilogue, rows, kw, pro=False):
     return _native.FTK_OK if ok else _native.FTK_ERR_INVALID
 
 
+#: (T, C, KW, U) the STAGE kind instantiates (K = 128 C KW): every epilogue, both prologue settings ...
+STAGE_EVEN = ((2, 4, 8, 2), (2, 4, 8, 4))
+#: ... store / argmax only, and the long K without the prologue.
+STAGE_ONE = ((1, 4, 8, 2), (1, 4, 8, 4))
+STAGE_LONG = ((1, 12, 8, 3), (1, 12, 8, 4))
+
+
+def _stage_status(m, k, epilogue, t, kw, u, pro=False):
+    if m > 16 or k % (128 * kw):
+        return _native.FTK_ERR_UNSUPPORTED
+    shapes = STAGE_EVEN + (() if epilogue == _native.EPI_SWIGLU else STAGE_ONE + (() if pro else STAGE_LONG))
+    return _native.FTK_OK if (t, k // (128 * kw), kw, u) in shapes else _native.FTK_ERR_INVALID
+
+
 def _configs(m):
     gemv = []
     if m <= 4:
@@ -168,6 +182,8 @@ def _configs(m):
                  for t, _, kw, u in MSTREAM_EVEN + MSTREAM_ONE for gpc in (1, 4)]
         gemv += [_native.Config(_native.KIND_QUAD, 4 * rs, 0, gpc, kw)
                  for rs, _, kw in QUAD_SHAPES + QUAD_ONE for gpc in (1, 8)]
+        gemv += [_native.Config(_native.KIND_STAGE, 16 * t, u, gpc, kw)
+                 for t, _, kw, u in STAGE_EVEN + STAGE_ONE + STAGE_LONG for gpc in (1, 4)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
             for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
     return [None] + gemv + mfma
@@ -183,7 +199,7 @@ def test_plan_writes_every_output_once(m, n, k):
             if cfg is not None and k % 8:
                 continue
             if (cfg is not None and epilogue == _native.EPI_SWIGLU
-                    and cfg.rows_per_wave in ((16,) if cfg.kind == _native.KIND_MFMA
+                    and cfg.rows_per_wave in ((16,) if cfg.kind in (_native.KIND_MFMA, _native.KIND_STAGE)
                                               else (4,) if cfg.kind == _native.KIND_QUAD else (1,))):
                 continue  # a SwiGLU workgroup / row group needs a gate row and its up row
             p = _native.Plan()
@@ -198,6 +214,11 @@ def test_plan_writes_every_output_once(m, n, k):
                     continue
             if cfg is not None and cfg.kind == _native.KIND_MFMA_STREAM:
                 want = _mstream_status(m, k, epilogue, cfg.rows_per_wave // 16, cfg.waves, cfg.unroll)
+                assert status == want, (m, n, k, epilogue, cfg)
+                if want != _native.FTK_OK:
+                    continue
+            if cfg is not None and cfg.kind == _native.KIND_STAGE:
+                want = _stage_status(m, k, epilogue, cfg.rows_per_wave // 16, cfg.waves, cfg.unroll)
                 assert status == want, (m, n, k, epilogue, cfg)
                 if want != _native.FTK_OK:
                     continue
@@ -222,6 +243,10 @@ def test_plan_writes_every_output_once(m, n, k):
                 t = p.rows_per_wave // 16
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
                 assert p.threads == 64 * p.waves and k % (32 * p.waves) == 0
+            if p.kind == _native.KIND_STAGE:
+                t = p.rows_per_wave // 16
+                assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
+                assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_QUAD:
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
                 assert p.unroll * 128 * p.waves == k and p.threads == 64 * max(4, p.waves)
@@ -244,17 +269,20 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
-    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # 4x4x4 MFMA blocks on the STREAM schedule
-    assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.unroll == 4 and p.grid == 256
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # 16x16x32 MFMA tiles fed through LDS
+    assert p.kind == _native.KIND_STAGE and p.threads == 512 and p.unroll == 2 and p.grid == 256
     _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # with the norm
     assert p.kind == _native.KIND_QUAD and p.rows_per_wave == 8 and p.waves == 8
-    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K at M <= 8
-    assert p.kind == _native.KIND_QUAD and p.waves == 8 and p.unroll == 12
-    _native.call("ftk_plan_project", 16, 4096, 4096, 0, 256, None, p)  # 16x16x32 MFMA tiles on the STREAM schedule
-    assert p.kind == _native.KIND_MFMA_STREAM and p.threads == 512 and p.unroll == 8
-    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # QKV: 4x4x4 blocks
+    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K: x streamed, 3 segments in flight
+    assert p.kind == _native.KIND_STAGE and p.waves == 8 and p.unroll == 3
+    _native.call("ftk_plan_project", 8, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # fused at 5..8: 4x4x4
     assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.rows_per_wave == 8
-    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # x streamed beside the weights
+    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STAGE and p.rows_per_wave == 16 and p.grid == 192
+    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
+    assert p.kind == _native.KIND_STAGE and p.unroll == 3
+    c = _native.Config(_native.KIND_MFMA_STREAM, 0, 0, 0, 0)  # x streamed beside the weights
+    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, c, p)
     assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 8 and p.unroll == 16
     # K = 12288 with the prologue has no MFMA_STREAM kernel: the 8-row STREAM kernel (8 waves split K)
     _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
@@ -269,9 +297,9 @@ def test_plan_kinds():
 
 def test_default_kind_for_8b_shapes():
     """The planner's choice at the Qwen3-8B shapes (from the MI355X sweep): STREAM at M = 1 and,
-    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD at M = 5..8
-    and for QKV to 16; MFMA_STREAM for the rest of 9..16 (the 8-row STREAM kernel where
-    K = 12288 has the prologue)."""
+    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD for the fused
+    projections at M = 5..8; STAGE for the rest of 5..16 (the 8-row STREAM kernel where K = 12288
+    has the prologue)."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -283,10 +311,10 @@ def test_default_kind_for_8b_shapes():
             quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
             if m < quad_early:
                 want = _native.KIND_STREAM
-            elif m <= 8 or name == "qkv":
+            elif m <= 8 and name in ("qkv", "gate_up", "lm_head"):
                 want = _native.KIND_QUAD
             else:
-                want = _native.KIND_MFMA_STREAM
+                want = _native.KIND_STAGE
             assert p.kind == want, (m, name, p.kind)
     # the prologue at K = 12288 has no QUAD shape that fits the registers: the 8-row STREAM kernel
     p = _native.Plan()
