@@ -251,6 +251,9 @@ def main():
     ap.add_argument("--profile-gate-up", type=int, default=0, metavar="PASSES",
                     help="profiling mode: only PASSES eager passes of the 36 gate/up + SwiGLU launches, "
                          "then one 1 GiB device copy as the counter reference")
+    ap.add_argument("--profile-rows", type=str, default="", metavar="M[,M...]",
+                    help="profiling mode: two eager passes of the 36-layer projection chain at each M rows "
+                         "(the C4 workload), then one 1 GiB device copy as the counter reference")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU form in this build "
@@ -265,6 +268,9 @@ def main():
     cfg = QWEN3_8B
     if args.profile_gate_up:
         profile_gate_up(cfg, dev, args.profile_gate_up)
+        return
+    if args.profile_rows:
+        profile_rows(cfg, dev, [int(m) for m in args.profile_rows.split(",")])
         return
     model = Model(cfg, dev)
     stage("Qwen3-8B weights resident")
@@ -347,6 +353,25 @@ def profile_gate_up(cfg, dev, passes):
     torch.cuda.synchronize()
     print(json.dumps({"mode": "profile-gate-up", "passes": passes, "launches": passes * cfg["layers"],
                       "bytes_per_launch": layer_bytes(cfg, 1)["gate_up"], "copy_bytes": 1 << 30}), flush=True)
+
+
+def profile_rows(cfg, dev, rows):
+    """Eager passes of the 36-layer projection chain at M rows (for rocprofv3 counter runs), plus a
+    copy of known size. Each layer is RMSNorm-prologue QKV, O, RMSNorm-prologue gate/up + SwiGLU, down."""
+    model = Model(cfg, dev, head=False)
+    for m in rows:
+        step = Step(model, m, dev, seed=m)
+        for p in range(2):
+            step.layers()
+            torch.cuda.synchronize()
+        print(f"profile M={m} done", flush=True)
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # reference kernel: reads and writes exactly 1 GiB
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "profile-rows", "rows": rows, "passes": 2, "layers": cfg["layers"],
+                      "bytes_per_layer": {str(m): layer_bytes(cfg, m) for m in rows}, "copy_bytes": 1 << 30}),
+          flush=True)
 
 
 def shapes_table(model8, step8, dev):
