@@ -5,10 +5,11 @@ Drop-in for engine/kernels/linear.py: ``linear(x, weight, split_ok=False)``,
 argument meaning and fallback rule (linear.py:484-523). FP32 accumulation and
 one rounding to BF16 (linear.py:1-6). Under them:
 
-  * M <= 4: an HBM-streaming GEMV (x resident in LDS, 16-byte non-temporal
-    weight loads, v_dot2_f32_bf16, DPP reductions);
-  * any other shape: the kind the C library's planner picks (ragged K or an
-    unaligned pointer takes a generic kernel with scalar loads).
+  * M = 1 (and plain projections to M = 4): an HBM-streaming GEMV (x slice in
+    registers, 16-byte non-temporal weight loads, v_dot2_f32_bf16, DPP reductions);
+  * M = 2..16: MFMA kinds (4x4x4 blocks fed straight from 4-row x 256-byte
+    loads, or 16x16x32 tiles fed through LDS), as the C library's planner picks;
+    ragged K or an unaligned pointer takes a generic kernel with scalar loads.
 
 ``split_ok`` is accepted for signature compatibility. The result is always a
 contiguous BF16 tensor, which the reference allows ("may be" a Split,
@@ -180,6 +181,14 @@ def _candidates(m, n, k):
         for kw in (1, 2, 4, 8):
             for gpc in (2, 4, 16, 32):
                 configs.append(_native.Config(_native.KIND_STREAM, rpw, 0, gpc, kw))
+    for rows in (4, 8, 16, 24):
+        for kw in (4, 8):
+            for gpc in (1, 2, 32):
+                configs.append(_native.Config(_native.KIND_QUAD, rows, 0, gpc, kw))
+    for rows in (16, 32):
+        for unroll in (2, 3, 4):
+            for gpc in (1, 2):
+                configs.append(_native.Config(_native.KIND_STAGE, rows, unroll, gpc, 8))
     for rows in (16, 32):
         for kw in (8, 16):
             for unroll in (2, 4, 8, 16):
