@@ -116,15 +116,16 @@ static MstreamDefault mstream_default(int64_t M, int epi, bool pro, int64_t N, i
 }
 
 // QUAD launch shape, from the M = 1..16 sweep of the Qwen3-8B shapes on MI355X:
-// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets)
-// and for lm_head at up to 4 rows, 24 for a projection with the prologue at up
-// to 4 rows (QKV), 8 otherwise; the first shape that fits the registers.
+// 8 waves split K; 16 rows per tile for SwiGLU (two gate and two up row sets),
+// 4 for lm_head (many short walks: the fewest registers), 24 for a projection
+// with the prologue at up to 4 rows (QKV), 8 otherwise; the first shape that
+// fits the registers.
 struct QuadDefault {
   int rows, kw;
 };
 static QuadDefault quad_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
   if (M < 1 || M > kQuadMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
-  const int want = (epi == FTK_EPI_SWIGLU || (epi == FTK_EPI_ARGMAX && M <= 4)) ? 16 : (pro && M <= 4) ? 24 : 8;
+  const int want = epi == FTK_EPI_SWIGLU ? 16 : epi == FTK_EPI_ARGMAX ? 4 : (pro && M <= 4) ? 24 : 8;
   const QuadDefault order[] = {{want, 8}, {8, 8}, {4, 8}, {want, 4}, {8, 4}, {4, 4}, {8, 16}};
   for (const QuadDefault& d : order)
     if (quad_supported((int)M, d.rows, (int)K, d.kw, epi, pro)) return d;
@@ -137,12 +138,12 @@ static int64_t quad_default_cap(int64_t M, int tiles, int cus) {
 }
 // Where QUAD beats the other kinds (MI355X, Qwen3-8B shapes): below 5 rows
 // (against STREAM) lm_head from 2 rows, SwiGLU from 3, any projection with the
-// prologue at 4; at 5..8 (against STAGE) the fused projections (prologue,
-// SwiGLU or argmax). From 9 rows STAGE's 16x16x32 tiles, a quarter of the MFMA
-// issue per byte, win everywhere.
+// prologue at 4; at 5..8 (against STAGE) the prologue projection without an
+// epilogue (QKV). Elsewhere from 5 rows STAGE's 16x16x32 tiles, a quarter of the
+// MFMA issue per byte, win.
 static bool quad_preferred(int64_t M, int epi, bool pro) {
   if (M > 8) return false;
-  if (M >= 5) return pro || epi != FTK_EPI_STORE;
+  if (M >= 5) return pro && epi == FTK_EPI_STORE;
   if (epi == FTK_EPI_ARGMAX) return M >= 2;
   if (epi == FTK_EPI_SWIGLU) return M >= 3;
   return pro && M >= 4;

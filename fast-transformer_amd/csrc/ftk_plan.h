@@ -122,11 +122,12 @@ FTK_HD int quad_segments(int k, int kw) { return (kw < 1 || k % (128 * kw)) ? 0 
 FTK_HD int quad_groups(int m) { return m < 1 ? 0 : m <= 4 ? 1 : m <= 8 ? 2 : m <= 16 ? 4 : 0; }
 // Whether a QUAD shape keeps its registers without spilling, estimated from the
 // gfx950 builds: the x slice (4 MQ C), the weight window (4 RS C), the
-// accumulators (4 RS MQ) and, with the prologue, what is live while it runs:
-// the residual, the gain and the normalisation's temporaries (6 MQ C + 4 C).
-// Where both would not fit, the window is issued after the prologue, so the two
-// peaks do not add. The cap is 248 registers (128 for a 16-wave workgroup);
-// shapes over it are not built.
+// accumulators (4 RS MQ) and, with the prologue, what is live while it runs
+// (the residual, the gain and temporaries: 6 MQ C + 4 C) and the gain kept
+// through the first tile, where the slice is normalised (4 C + 24). Where the
+// prologue and the window would not fit together, the window is issued after
+// the prologue. The cap is 248 registers (128 for a 16-wave workgroup); shapes
+// over it are not built.
 constexpr int quad_cap(int kw) { return kw >= 16 ? 128 : 248; }
 constexpr int quad_main_regs(int mq, int rs, int c) { return 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32; }
 // With the prologue: issue the first weight window only after it, where the two
@@ -136,11 +137,11 @@ constexpr bool quad_late(int mq, int rs, int c, int kw, bool pro) {
 }
 constexpr bool quad_fits(int mq, int rs, int c, int kw, bool pro) {
   const int main_loop = quad_main_regs(mq, rs, c);
-  const int prologue = 10 * mq * c + 4 * c + 32;
-  const int est = !pro ? main_loop
-                       : quad_late(mq, rs, c, kw, pro) ? (main_loop > prologue ? main_loop : prologue)
-                                                       : main_loop + 6 * mq * c + 4 * c;
-  return est <= quad_cap(kw);
+  if (!pro) return main_loop <= quad_cap(kw);
+  // The slice is normalised during the first tile, so the gain stays live there.
+  const int first_tile = main_loop + 4 * c + 24;
+  const int prologue = quad_late(mq, rs, c, kw, pro) ? 10 * mq * c + 4 * c + 32 : main_loop + 6 * mq * c + 4 * c;
+  return (first_tile > prologue ? first_tile : prologue) <= quad_cap(kw);
 }
 
 // ---- M = 5..16 with K = 128 C KW: the STAGE kind (16x16x32 MFMA via LDS) -----

@@ -142,7 +142,8 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
   };
   if constexpr (!LATE) first_window();
 
-  // ---- RMSNorm prologue: normalise the slice in registers ---------------------
+  // ---- RMSNorm prologue: the row scales ----------------------------------------
+  float scale[MQ];
   if constexpr (PRO) {
     // Row m's sum of squares: each lane over its segments in order, the 16
     // lanes of the row, then the KW waves of the row group in wave order.
@@ -164,7 +165,6 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
           for (int j = 0; j < C; ++j) store16(a.sum + (size_t)(4 * q + i4) * K + first + j * kStep, xr[q][j]);
     }
     __syncthreads();
-    float scale[MQ];
 #pragma unroll
     for (int q = 0; q < MQ; ++q) {
       float total = red[grp * KW][4 * q + i4];
@@ -172,14 +172,9 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
       for (int w = 1; w < KW; ++w) total += red[grp * KW + w][4 * q + i4];
       scale[q] = 1.0f / sqrtf(total / (float)K + a.eps);
     }
-    // The gain of a chunk is widened once for the MQ rows that use it.
-#pragma unroll
-    for (int j = 0; j < C; ++j) {
-      float gf[8];
-      widen8(gv[j], gf);
-#pragma unroll
-      for (int q = 0; q < MQ; ++q) xr[q][j] = norm8w(xr[q][j], gf, scale[q]);
-    }
+    // Only the scales are found here: each K segment of the slice is normalised
+    // in the first tile right before its MFMAs, so that VALU work overlaps the
+    // weight stream instead of delaying it.
   }
   if constexpr (LATE) first_window();
 
@@ -197,6 +192,14 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
       for (int q = 0; q < MQ; ++q) acc[r][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < C; ++j) {
+      if constexpr (PRO) {
+        if (count == 0) {  // first tile: normalise this segment of the slice in place
+          float gf[8];
+          widen8(gv[j], gf);  // the gain of a chunk, widened once for the MQ rows that use it
+#pragma unroll
+          for (int q = 0; q < MQ; ++q) xr[q][j] = norm8w(xr[q][j], gf, scale[q]);
+        }
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll

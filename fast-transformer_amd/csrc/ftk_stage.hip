@@ -25,8 +25,11 @@
 //     chunk 4 s + l / 16). Only this wave touches that memory, so no barrier:
 //     a wave's LDS instructions execute in order.
 //   * The x slice (B operand, lane l: x row l % 16 at the same k) is resident in
-//     registers (normalised there with the prologue), or, for the long K without
-//     the prologue, streamed beside the weights with the same lookahead.
+//     registers, or, for the long K without the prologue, streamed beside the
+//     weights with the same lookahead. With the prologue the row scales are found
+//     first (sums of squares, one barrier), and each K segment of the slice is
+//     normalised in the first tile right before its MFMAs, with the gain read
+//     from LDS: that VALU work overlaps the weight stream instead of delaying it.
 //   * Per-tile 16 x 16 partials wait in LDS; one barrier at the end, then the
 //     workgroup sums the KW partials in wave order (deterministic) and runs the
 //     epilogue on every output of its tiles.
@@ -46,6 +49,8 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
   __shared__ u32x4_t stage[KW][256];          // one subtile's 16 rows x 16 chunks per wave
   __shared__ float red[KW][16];
   __shared__ unsigned long long best_lds[KW][16];
+  constexpr int GCH = PRO ? 16 * C * KW : 1;  // 16-byte chunks of the RMSNorm gain (K / 8)
+  __shared__ u32x4_t gain[GCH];
 
   const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
   const int i4 = lane & 3, cb = lane >> 2;   // load layout: row i4 of a row set, chunk cb
@@ -61,7 +66,17 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
   auto slot_of = [](int row, int chunk) { return row * 16 + (chunk ^ (4 * (row & 3) + (row >> 2))); };
   u32x4_t* st = stage[kw];
 
-  // ---- the x slice: resident (normalised in place with the prologue) -----------
+  // ---- the gain first (for LDS), then the x slice (normalised in place with the
+  // prologue) -----------------------------------------------------------------------
+  constexpr int GPT = (GCH + 64 * KW - 1) / (64 * KW);  // gain chunks per thread
+  u32x4_t gload[PRO ? GPT : 1];
+  if constexpr (PRO) {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int c = tid + i * 64 * KW;
+      if (c < GCH) gload[i] = load16(a.gamma + (size_t)c * 8);
+    }
+  }
   // With the prologue, row li is x[li] or the gathered x[x_ids[li]], plus the residual.
   const uint16_t* xrow = (PRO && mine) ? x_row(a, li) : a.x + (size_t)(mine ? li : 0) * K;
   auto x_frag = [&](int j, int s) { return mine ? load16(xrow + xoff(j, s)) : u32x4_t{0u, 0u, 0u, 0u}; };
@@ -100,8 +115,16 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
     }
   }
 
-  // ---- RMSNorm prologue: row sums of squares over (wave, quarter, step) in order --
+  // ---- RMSNorm prologue: row sums of squares over (wave, quarter, step) in order.
+  // Only the scale is found here; each K segment is normalised in the first tile,
+  // right before its MFMAs, so that work overlaps the weight stream. -------------
+  float scale = 0.f;
   if constexpr (PRO) {
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int c = tid + i * 64 * KW;
+      if (c < GCH) gain[c] = gload[i];
+    }
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < C; ++j)
@@ -121,13 +144,7 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
     float total = red[0][li];
 #pragma unroll
     for (int w = 1; w < KW; ++w) total += red[w][li];
-    const float scale = 1.0f / sqrtf(total / (float)K + a.eps);
-    // The gain is loaded only now (cache hits behind the weight window), so its
-    // registers are never live beside the window's.
-#pragma unroll
-    for (int j = 0; j < C; ++j)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xr[j][s] = norm8(xr[j][s], load16(a.gamma + xoff(j, s)), scale);
+    scale = 1.0f / sqrtf(total / (float)K + a.eps);
   }
 
   // ---- tiles: stage each unit through LDS into the MFMAs, refill the window ------
@@ -143,6 +160,12 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
 #pragma unroll
     for (int j = 0; j < C; ++j) {
       const int q = j % U;
+      if constexpr (PRO) {
+        if (count == 0) {  // first tile: normalise this segment of the slice in place
+#pragma unroll
+          for (int s = 0; s < 4; ++s) xr[j][s] = norm8(xr[j][s], gain[xoff(j, s) >> 3], scale);
+        }
+      }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
 #pragma unroll

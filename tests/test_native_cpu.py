@@ -138,10 +138,12 @@ def _quad_fits(mq, rs, c, kw, pro):
     """The register estimate of the QUAD kind (x slice, weight window, accumulators, prologue inputs)."""
     cap = 128 if kw >= 16 else 248
     main_loop = 4 * mq * c + 4 * rs * c + 4 * rs * mq + 32
-    prologue = 10 * mq * c + 4 * c + 32
-    late = pro and main_loop + 6 * mq * c + 4 * c > cap  # the window waits for the prologue
-    est = main_loop if not pro else max(main_loop, prologue) if late else main_loop + 6 * mq * c + 4 * c
-    return est <= cap
+    if not pro:
+        return main_loop <= cap
+    first_tile = main_loop + 4 * c + 24  # the gain lives through the first tile (normalised there)
+    late = main_loop + 6 * mq * c + 4 * c > cap  # the window waits for the prologue
+    prologue = 10 * mq * c + 4 * c + 32 if late else main_loop + 6 * mq * c + 4 * c
+    return max(first_tile, prologue) <= cap
 
 
 def _quad_status(m, k, epilogue, rows, kw, pro=False):
@@ -297,9 +299,9 @@ def test_plan_kinds():
 
 def test_default_kind_for_8b_shapes():
     """The planner's choice at the Qwen3-8B shapes (from the MI355X sweep): STREAM at M = 1 and,
-    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD for the fused
-    projections at M = 5..8; STAGE for the rest of 5..16 (the 8-row STREAM kernel where K = 12288
-    has the prologue)."""
+    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD for QKV at
+    M = 5..8; STAGE for the rest of 5..16 (the 8-row STREAM kernel where K = 12288 has the
+    prologue)."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -311,7 +313,7 @@ def test_default_kind_for_8b_shapes():
             quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
             if m < quad_early:
                 want = _native.KIND_STREAM
-            elif m <= 8 and name in ("qkv", "gate_up", "lm_head"):
+            elif (m <= 8 and name == "qkv") or m <= 4:
                 want = _native.KIND_QUAD
             else:
                 want = _native.KIND_STAGE
