@@ -360,6 +360,52 @@ static int64_t call_workspace(const ftk_plan& p, int epi, bool pro) {
   return 0;
 }
 
+// ---- decode attention: launch planning --------------------------------------
+
+// Workgroups the default split count aims at: two per CU, so the cache rows of
+// a short context are all in flight at once.
+constexpr int kAttnGroupsPerCu = 2;
+
+static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, int cus, const ftk_attn_config* cfg,
+                     ftk_attn_plan* p, AttnShape* shape) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || C < 1 || Hq % Hkv || cus < 1) return FTK_ERR_INVALID;
+  const int64_t G = Hq / Hkv;
+  if ((D != 64 && D != 128) || G > kAttnMaxGroup) return FTK_ERR_UNSUPPORTED;
+  if (C > INT32_MAX / 2 || B * Hkv > INT32_MAX / 2) return FTK_ERR_INVALID;
+  const int groups = (int)(B * Hkv);
+  int kind = cfg && cfg->kind ? cfg->kind : (D == 128 && G <= 4 ? FTK_ATTN_QUAD : FTK_ATTN_ROWS);
+  const int waves = cfg && cfg->waves ? cfg->waves : 4;
+  int unroll = cfg && cfg->unroll ? cfg->unroll : (kind == FTK_ATTN_QUAD ? 2 : 4);
+  if (kind == FTK_ATTN_ROWS && !(cfg && cfg->unroll) && !attn_supported(kind, (int)D, (int)G, waves, unroll))
+    unroll = 2;
+  if (!attn_supported(kind, (int)D, (int)G, waves, unroll)) return FTK_ERR_INVALID;
+  const int64_t unit = kind == FTK_ATTN_QUAD ? 16 : (64 / (D / 8)) * unroll;  // slots one wave takes per step
+  int64_t splits;
+  if (cfg && cfg->splits) {
+    if (cfg->splits < 1) return FTK_ERR_INVALID;
+    splits = cfg->splits < C ? cfg->splits : C;
+    if (splits > kAttnMaxSplits) return FTK_ERR_INVALID;
+  } else {
+    const int64_t want = ((int64_t)kAttnGroupsPerCu * cus + groups - 1) / groups;
+    const int64_t most = (C + waves * unit - 1) / (waves * unit);  // at least one step per wave
+    splits = want < most ? want : most;
+    if (splits > kAttnMaxSplits) splits = kAttnMaxSplits;
+    if (splits < 1) splits = 1;
+  }
+  const int64_t chunk = (C + splits - 1) / splits;
+  splits = (C + chunk - 1) / chunk;  // no interval lies wholly past the cache
+  if ((int64_t)groups * splits > INT32_MAX) return FTK_ERR_INVALID;
+  p->kind = kind;
+  p->splits = (int)splits;
+  p->chunk = (int)chunk;
+  p->waves = waves;
+  p->unroll = unroll;
+  p->grid = (int)(groups * splits);
+  p->workspace_bytes = splits > 1 ? (int64_t)groups * splits * G * (D + 2) * 4 : 0;
+  if (shape) *shape = AttnShape{kind, (int)D, (int)G, groups, (int)splits, (int)chunk, waves, unroll};
+  return FTK_OK;
+}
+
 }  // namespace ftk
 
 using namespace ftk;
@@ -667,6 +713,57 @@ int ftk_argmax_bf16(const void* logits, int64_t rows, int64_t vocab, void* ids, 
   if (workspace == nullptr || workspace_bytes < ftk_argmax_workspace_bytes(rows, vocab)) return FTK_ERR_WORKSPACE;
   return hip_status(launch_argmax((const uint16_t*)logits, (int)rows, (int)vocab, ids, ids_bytes, top,
                                   (unsigned long long*)workspace, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int ftk_plan_decode_attention(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity, int64_t dim,
+                              int compute_units, const ftk_attn_config* cfg, ftk_attn_plan* plan) {
+  if (!plan) return FTK_ERR_INVALID;
+  return attn_plan(batch, q_heads, kv_heads, capacity, dim, compute_units, cfg, plan, nullptr);
+}
+
+int64_t ftk_decode_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                                             int64_t dim, const ftk_attn_config* cfg) {
+  DeviceInfo d = device_info();
+  ftk_attn_plan p;
+  if (!d.ok || attn_plan(batch, q_heads, kv_heads, capacity, dim, d.cus, cfg, &p, nullptr) != FTK_OK) return -1;
+  return p.workspace_bytes;
+}
+
+int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const int64_t* position,
+                              int positions, void* out, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                              int64_t capacity, int64_t dim, double scale, void* workspace, int64_t workspace_bytes,
+                              const ftk_attn_config* cfg, void* stream) {
+  if (!q || !k || !v || !position || !out) return FTK_ERR_INVALID;
+  if (positions != 1 && positions != batch) return FTK_ERR_INVALID;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return FTK_ERR_UNSUPPORTED;
+  DeviceInfo d = device_info();
+  if (!d.ok) return FTK_ERR_INVALID;
+  ftk_attn_plan p;
+  AttnShape shape;
+  const int st = attn_plan(batch, q_heads, kv_heads, capacity, dim, d.cus, cfg, &p, &shape);
+  if (st != FTK_OK) return st;
+  float* partial = nullptr;
+  float* stats = nullptr;
+  if (p.splits > 1) {
+    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned16(workspace)) return FTK_ERR_WORKSPACE;
+    partial = (float*)workspace;
+    stats = partial + (size_t)shape.groups * p.splits * shape.group_size * dim;
+  }
+  AttnArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.position = position;
+  a.pos_stride = (positions == 1 && batch > 1) ? 0 : 1;
+  a.out = (uint16_t*)out;
+  a.partial = partial;
+  a.stats = stats;
+  a.kv_heads = (int)kv_heads;
+  a.capacity = (int)capacity;
+  a.splits = p.splits;
+  a.chunk = p.chunk;
+  a.scale_log2 = (float)(scale * 1.4426950408889634);
+  return hip_status(launch_attention(a, shape, reinterpret_cast<hipStream_t>(stream)));
 }
 
 int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream) {

@@ -141,6 +141,17 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                  0, 0, 0);
 }
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// D += A B on the 16-block 4x4x4 BF16 MFMA. Lane 4 b + i holds A_b[i][0..3]
+// (four BF16 in two dwords), lane 4 b + j holds B_b[0..3][j], and lane 4 b + j
+// receives D_b[r][j] in element r.
+__device__ __forceinline__ f32x4_t mfma4x4x4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  const u32x2_t a = {a0, a1}, b = {b0, b1};
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c,
+                                                0, 0, 0);
+}
+
 // Streaming 16-byte load: weights are read exactly once per call.
 __device__ __forceinline__ u32x4_t load_stream16(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
@@ -172,6 +183,16 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
 __device__ __forceinline__ float wave_sum(float v) {
   v = wave_sum_to_last(v);
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over lane bits 2..5 of one value per lane (a column of the 16-block MFMA
+// layout), the same bits in every lane of the column.
+__device__ __forceinline__ float quad_lane_sum(float v) {
+  v += dpp<0x128, 0xF>(v);
+  v += dpp<0x124, 0xF>(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
 }
 
 // Greedy-argmax key: larger key = larger BF16 value, then lower index.

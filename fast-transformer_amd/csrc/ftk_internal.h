@@ -123,6 +123,39 @@ struct MfmaArgs {
 bool mfma_supported(int M, int t, int unroll, int waves, int epi);
 hipError_t launch_mfma(const ProjArgs& a, int epi, const MfmaShape& shape, const MfmaArgs& p, hipStream_t stream);
 
+// Arguments of one split-KV decode-attention launch (engine/kernels/decode_attention.py:31-149).
+// A group is one (row, KV head) pair: group = row * kv_heads + kv_head.
+struct AttnArgs {
+  const uint16_t* q;        // [groups * G, D] BF16: the G query heads of each group, head-major
+  const uint16_t* k;        // [groups, capacity, D] BF16 (the [B, Hkv, C, D] cache)
+  const uint16_t* v;        // same layout as k
+  const int64_t* position;  // newest cache slot: position[pos_stride * row]
+  int pos_stride;           // 0: one position for every row; 1: one per row
+  uint16_t* out;            // [groups * G, D] BF16
+  float* partial;           // [groups, splits, G, D] FP32 numerators (splits > 1 only)
+  float* stats;             // [groups, splits, G, 2] FP32 (max, denominator) (splits > 1 only)
+  int kv_heads;
+  int capacity;             // cache slots per group
+  int splits, chunk;        // slot intervals per group and slots per interval
+  float scale_log2;         // scale * log2(e), formed in double
+};
+
+// Launch shape of the decode attention.
+struct AttnShape {
+  int kind;        // FTK_ATTN_ROWS or FTK_ATTN_QUAD
+  int dim;         // D: 64 or 128
+  int group_size;  // G: query heads per KV head (1..kAttnMaxGroup)
+  int groups;      // rows * KV heads
+  int splits;      // slot intervals per group (1: the partials kernel writes the output)
+  int chunk;       // slots per interval
+  int waves;       // W: waves per workgroup (4, 8)
+  int unroll;      // U: cache-row loads of K (and of V) in flight per lane (2, 4, 8)
+};
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnMaxSplits = 1024;  // slot intervals per group the merge kernel takes
+bool attn_supported(int kind, int dim, int group_size, int waves, int unroll);
+hipError_t launch_attention(const AttnArgs& a, const AttnShape& s, hipStream_t stream);
+
 // Greedy-argmax second stage: ids[m] (and top[m]) from keys[slot * M + m], slot < slots.
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream);

@@ -33,17 +33,6 @@
 
 namespace ftk {
 
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-
-// D += A B on the 16-block 4x4x4 BF16 MFMA. Lane 4 b + i holds A_b[i][0..3]
-// (four BF16 in two dwords), lane 4 b + j holds B_b[0..3][j], and lane 4 b + j
-// receives D_b[r][j] in element r.
-__device__ __forceinline__ f32x4_t mfma4x4x4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
-  const u32x2_t a = {a0, a1}, b = {b0, b1};
-  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c,
-                                                0, 0, 0);
-}
-
 // Sum of a 16-block accumulator over its blocks (lane bits 2..5). Lane l
 // returns the total of element (l >> 4) & 3 for x column l & 3; lanes that
 // differ only in bits 2 and 3 return the same bits.
@@ -59,16 +48,6 @@ __device__ __forceinline__ float quad_block_sum(f32x4_t v, int lane) {
   w += dpp<0x128, 0xF>(w);  // row_ror:8
   w += dpp<0x124, 0xF>(w);  // row_ror:4
   return w;
-}
-
-// Sum over lane bits 2..5 of one value per lane (the RMSNorm sums of squares),
-// the same bits in every lane of a column.
-__device__ __forceinline__ float quad_lane_sum(float v) {
-  v += dpp<0x128, 0xF>(v);
-  v += dpp<0x124, 0xF>(v);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
 }
 
 // MQ: groups of 4 x rows the kernel is built for (a.M <= 4 MQ are real; the

@@ -18,6 +18,7 @@ FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = r
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
 PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
 KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE = range(8)
+ATTN_AUTO, ATTN_ROWS, ATTN_QUAD = range(3)
 MAX_ROWS = 32
 
 _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -49,6 +50,23 @@ class Rows(ctypes.Structure):
     _fields_ = [("residual", _c_void_p), ("sum", _c_void_p), ("x_ids", _c_void_p), ("x_ids_bytes", _int)]
 
 
+class AttnConfig(ctypes.Structure):
+    """ftk_attn_config: a decode-attention launch choice (kind, splits, waves, unroll); zeros = planner default."""
+
+    _fields_ = [("kind", _int), ("splits", _int), ("waves", _int), ("unroll", _int)]
+
+    def key(self):
+        return (self.kind, self.splits, self.waves, self.unroll)
+
+    def __repr__(self):
+        return f"AttnConfig{self.key()}"
+
+
+class AttnPlan(ctypes.Structure):
+    _fields_ = [("kind", _int), ("splits", _int), ("chunk", _int), ("waves", _int), ("unroll", _int),
+                ("grid", _int), ("workspace_bytes", _i64)]
+
+
 # name -> (restype, argtypes), exactly the declarations of include/ftk.h
 SIGNATURES = {
     "ftk_version": (ctypes.c_char_p, []),
@@ -77,6 +95,12 @@ SIGNATURES = {
     "ftk_merge_splits_bf16": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
     "ftk_argmax_workspace_bytes": (_i64, [_i64, _i64]),
     "ftk_project_workspace_bytes": (_i64, [_i64, _i64, _i64, _int, ctypes.POINTER(Config)]),
+    "ftk_decode_attention_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p, _i64, _i64,
+                                         _i64, _i64, _i64, ctypes.c_double, _c_void_p, _i64,
+                                         ctypes.POINTER(AttnConfig), _c_void_p]),
+    "ftk_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(AttnConfig)]),
+    "ftk_plan_decode_attention": (_int, [_i64, _i64, _i64, _i64, _i64, _int, ctypes.POINTER(AttnConfig),
+                                         ctypes.POINTER(AttnPlan)]),
     "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
     "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
                                  ctypes.POINTER(_i64)]),

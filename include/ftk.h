@@ -210,7 +210,55 @@ int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, v
 /* Workspace bytes of ftk_argmax_bf16 for `rows` rows of `vocab` logits. */
 int64_t ftk_argmax_workspace_bytes(int64_t rows, int64_t vocab);
 
+/* ---- decode attention ------------------------------------------------------------ */
+/* Launch choice of the split-KV decode attention (the reference's layout tuple
+ * `block_n, splits, warps`, engine/kernels/decode_attention.py:152-157).
+ * Zero fields mean "planner default". */
+typedef enum ftk_attn_kind {
+  FTK_ATTN_AUTO = 0,
+  FTK_ATTN_ROWS = 1,  /* any D in {64, 128}, up to 8 query heads per KV head: v_dot2 scores summed
+                         over each cache row's lanes, an online softmax per lane, p V on the VALU */
+  FTK_ATTN_QUAD = 2   /* D = 128, up to 4 query heads per KV head: scores on 16-block 4x4x4 MFMAs fed
+                         by 4 cache rows x 256 bytes per wave load, one softmax step per (row, head),
+                         p V on the VALU */
+} ftk_attn_kind;
+typedef struct ftk_attn_config {
+  int kind;    /* ftk_attn_kind */
+  int splits;  /* slot intervals per (row, KV head), at most 1024; 1 = no merge launch */
+  int waves;   /* waves per workgroup (4, 8) */
+  int unroll;  /* ROWS: cache rows of K (and of V) in flight per lane per step (2, 4, 8);
+                  QUAD: 16-row units a wave has in flight beyond the one it computes (1, 2) */
+} ftk_attn_config;
+typedef struct ftk_attn_plan {
+  int kind;
+  int splits;               /* slot intervals per (row, KV head) */
+  int chunk;                /* slots per interval */
+  int waves;
+  int unroll;
+  int grid;                 /* partials workgroups: rows * KV heads * splits */
+  int64_t workspace_bytes;  /* FP32 partials + (max, denominator) pairs; 0 when splits = 1 */
+} ftk_attn_plan;
+/* out = softmax(q k^T * scale) v over the cache slots 0..position of each row,
+ * for a one-token decode query: q [B, Hq, D] (the reference's [B, Hq, 1, D]),
+ * k, v [B, Hkv, C, D], out [B, Hq, D] (the reference's [B, 1, Hq, D]); BF16.
+ * Query head h reads KV head h / (Hq / Hkv). `position` is int64: one slot
+ * index for every row (positions = 1, the reference's [1] tensor) or one per
+ * row (positions = B). Slots past min(position, C - 1) are never read into
+ * the result (they may hold NaN). Scores and sums are FP32; p is rounded to
+ * BF16 before it weights V. D is 64 or 128; Hq / Hkv <= 8; q, k, v, out
+ * 16-byte aligned. Replaces decode_attention and its kernels
+ * (engine/kernels/decode_attention.py:31-149, :229-258). */
+int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const int64_t* position, int positions,
+                              void* out, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                              int64_t dim, double scale, void* workspace, int64_t workspace_bytes,
+                              const ftk_attn_config* cfg, void* stream);
+/* Workspace bytes of that call on the current device (-1: invalid shape or no device). */
+int64_t ftk_decode_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
+                                             int64_t dim, const ftk_attn_config* cfg);
 /* ---- planning (host only, no device needed) ---------------------------------- */
+/* The launch ftk_decode_attention_bf16 would make on `compute_units` CUs. */
+int ftk_plan_decode_attention(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity, int64_t dim,
+                              int compute_units, const ftk_attn_config* cfg, ftk_attn_plan* plan);
 
 /* The launch ftk_project_bf16 would make for this shape on `compute_units` CUs
  * (`epilogue` | FTK_PLAN_PROLOGUE for a call with gamma). */
