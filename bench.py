@@ -15,7 +15,8 @@ value = algorithmic bytes of the step / step time (GB/s). Rank 0 prints one
 JSON line with the contract fields plus ``roofline`` (dominant kernel: the
 fused gate/up + SwiGLU GEMV), ``cpu_baseline`` (the reference's torch CPU path on
 a bounded sample of the same workload) and ``per_shape`` (µs, GB/s and fraction
-of the 8 TB/s HBM roofline for every BASELINE configuration).
+of the 8 TB/s HBM roofline for every BASELINE configuration, plus the split-KV
+decode attention at Qwen3-8B heads).
 """
 
 import argparse
@@ -33,6 +34,7 @@ sys.path.insert(0, str(ROOT / "fast-transformer_amd"))
 
 from kernels import _native  # noqa: E402
 from kernels import argmax as A  # noqa: E402
+from kernels import decode_attention as DA  # noqa: E402
 from kernels import linear as L  # noqa: E402
 from kernels import swiglu as S  # noqa: E402
 
@@ -311,6 +313,7 @@ def main():
     stage(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
     if not args.no_shapes:
         per_shape = shapes_table(model, step, dev)
+        per_shape.update(attention_table(cfg, dev))
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -421,6 +424,30 @@ def shapes_table(model8, step8, dev):
     us = time_graph(g) / 64
     out["C1 0.6B qkv M=1 (no prologue)"] = shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096)
     del model06, copies
+    return out
+
+
+#: Decode attention next to the projections (Qwen3-8B heads: 32 query, 8 KV, D = 128):
+#: (rows, cache slots, distinct caches timed in one graph: together over the 256 MB MALL).
+ATTN_CASES = ((1, 4096, 36), (1, 32768, 8), (16, 4096, 4))
+
+
+def attention_table(cfg, dev):
+    """µs / GB/s / fraction of the HBM roofline of decode_attention over full caches (all slots valid)."""
+    out = {}
+    hq, hkv, d = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
+    for b, c, copies in ATTN_CASES:
+        g = torch.Generator(device=dev).manual_seed(11)
+        ks = [torch.randn((b, hkv, c, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+        vs = [torch.randn((b, hkv, c, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+        q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.bfloat16)
+        pos = torch.tensor([c - 1], device=dev, dtype=torch.int64)
+        graph = capture(lambda: [DA.decode_attention(q, k, v, pos, d ** -0.5) for k, v in zip(ks, vs)])
+        us = time_graph(graph) / copies
+        byts = 2 * b * hkv * c * d * 2 + 2 * 2 * b * hq * d
+        out[f"attention 8B decode B={b} C={c}"] = shape_entry(us, byts)
+        del ks, vs, graph
+        stage(f"attention B={b} C={c} done")
     return out
 
 

@@ -246,14 +246,15 @@ __device__ __forceinline__ float head_max(float v) {
   return fmaxf(v, __shfl_xor(v, 32));
 }
 
-template <int G, int W, int PF>
+template <int G, int W, int NG>
 __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
-  constexpr int D = 128, SLOTS = 16;
+  constexpr int D = 128, SLOTS = 16 * NG;  // a unit: NG groups of 16 cache rows
   __shared__ float p_lds[W][64];
   __shared__ float acc_lds[W][G][D];
   __shared__ float m_lds[W][G], l_lds[W][G];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: loop tests stay scalar
   const int i4 = lane & 3, chunk = lane >> 2;
   const int group = blockIdx.x / a.splits, split = blockIdx.x - group * a.splits;
   const int row = group / a.kv_heads;
@@ -263,12 +264,17 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
   const int end = (int)(begin + a.chunk < visible ? begin + a.chunk : visible);
   const int units = end > begin ? (end - begin + SLOTS - 1) / SLOTS : 0;
 
-  const size_t cache = (size_t)group * a.capacity * D + chunk * 8;
-  const uint16_t* kb = a.k + cache;
-  const uint16_t* vb = a.v + cache;
+  // K and V through buffer descriptors whose range ends at row `end`: a load
+  // of a later row returns zeros without touching memory. So the ragged last
+  // unit needs no value masking (and never reads the NaN a stale slot may
+  // hold), and the next-unit loads of the last step cost nothing.
+  const size_t cache = (size_t)group * a.capacity * D;
+  const uint32_t limit = end > 0 ? (uint32_t)end * (D * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k + cache), 0, limit, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v + cache), 0, limit, kBufferFlags);
   const u32x4_t zero = {0u, 0u, 0u, 0u};
   const u32x4_t qv = i4 < G ? load16(a.q + ((size_t)group * G + i4) * D + chunk * 8) : zero;
-  const int srow = 4 * ((lane >> 2) & 3) + ((lane >> 4) & 3);  // unit row of this lane's score
+  const int srow = 4 * ((lane >> 2) & 3) + ((lane >> 4) & 3);  // row of this lane's score in a group
 
   float m = -INFINITY, l = 0.f;  // head (lane & 3)'s softmax state, the same in its 16 lanes
   float acc[G][8];               // numerators of this chunk's 8 dimensions, over rows i4 of each load
@@ -277,84 +283,77 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 
-  auto load_unit = [&](int unit, u32x4_t (&kr)[4], u32x4_t (&vr)[4]) {
-    const int first = begin + unit * SLOTS + i4;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = first + 4 * u < end ? first + 4 * u : end - 1;  // rows past the end: read, then masked
-      kr[u] = load_stream16(kb + (size_t)t * D);
-      vr[u] = load_stream16(vb + (size_t)t * D);
-    }
+  // Byte offset of this lane's chunk in load u of group g of a unit. Each load
+  // goes into the register its predecessor just freed.
+  auto at = [&](int unit, int g, int u) {
+    return (uint32_t)(begin + unit * SLOTS + 16 * g + 4 * u + i4) * (D * 2) + chunk * 16;
   };
 
-  auto process = [&](int unit, const u32x4_t (&kr)[4], const u32x4_t (&vr)[4]) {
-    const int base = begin + unit * SLOTS;
-    f32x4_t sc[4];
+  u32x4_t kr[NG][4], vr[NG][4];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      sc[u] = mfma4x4x4(kr[u][0], kr[u][1], qv[0], qv[1], z);
-      sc[u] = mfma4x4x4(kr[u][2], kr[u][3], qv[2], qv[3], sc[u]);
+      kr[g][u] = buffer_load16(krs, at(wave, g, u));
+      vr[g][u] = buffer_load16(vrs, at(wave, g, u));
     }
-    const float dot = quad_transpose_sum(sc, lane);
-    const float s = base + srow < end ? dot * a.scale_log2 : -INFINITY;
-    const float top = fmaxf(m, head_max(s));
-    const float pivot = top == -INFINITY ? 0.f : top;
-    const float corr = exp2_f32(m - pivot);
-    const float p = exp2_f32(s - pivot);
-    l = l * corr + quad_lane_sum(p);
-    m = top;
+  for (int unit = wave; unit < units; unit += W) {
+    const int next = unit + W;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int base = begin + unit * SLOTS + 16 * g;
+      f32x4_t sc[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+        sc[u] = mfma4x4x4(kr[g][u][0], kr[g][u][1], qv[0], qv[1], z);
+        sc[u] = mfma4x4x4(kr[g][u][2], kr[g][u][3], qv[2], qv[3], sc[u]);
+        kr[g][u] = buffer_load16(krs, at(next, g, u));
+      }
+      const float dot = quad_transpose_sum(sc, lane);
+      const float s = base + srow < end ? dot * a.scale_log2 : -INFINITY;
+      const float top = fmaxf(m, head_max(s));
+      const float pivot = top == -INFINITY ? 0.f : top;
+      const float corr = exp2_f32(m - pivot);
+      const float p = exp2_f32(s - pivot);
+      l = l * corr + quad_lane_sum(p);
+      m = top;
 
-    // The BF16 weights to the V lanes: lane 4 b + i needs rows 4 u + i, every head.
-    p_lds[wave][lane] = round_bf16(p);
-    __builtin_amdgcn_wave_barrier();
-    float pb[4][G];
+      // The BF16 weights to the V lanes: lane 4 b + i needs rows 4 u + i, every head.
+      p_lds[wave][lane] = round_bf16(p);
+      __builtin_amdgcn_wave_barrier();
+      float pb[4][G];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(&p_lds[wave][16 * i4 + 4 * u]);
+      for (int u = 0; u < 4; ++u) {
+        const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(&p_lds[wave][16 * i4 + 4 * u]);
 #pragma unroll
-      for (int h = 0; h < G; ++h) pb[u][h] = v4[h];
-    }
-    __builtin_amdgcn_wave_barrier();
+        for (int h = 0; h < G; ++h) pb[u][h] = v4[h];
+      }
+      __builtin_amdgcn_wave_barrier();
 
-    float cs[G];
-    bool rescale = false;
+      float cs[G];
+      bool rescale = false;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      cs[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
-      rescale |= cs[h] != 1.f;
-    }
-    if (rescale) {
+      for (int h = 0; h < G; ++h) {
+        cs[h] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
+        rescale |= cs[h] != 1.f;
+      }
+      if (rescale) {
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] *= cs[h];
-    }
-    const bool full = base + SLOTS <= end;
+          for (int e = 0; e < 8; ++e) acc[h][e] *= cs[h];
+      }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float vf[8];
-      widen8(full || base + 4 * u + i4 < end ? vr[u] : zero, vf);
+      for (int u = 0; u < 4; ++u) {
+        float vf[8];
+        widen8(vr[g][u], vf);
+        vr[g][u] = buffer_load16(vrs, at(next, g, u));
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] += pb[u][h] * vf[e];
-    }
-  };
-
-  // A ring of PF + 1 unit buffers: the loads of the PF units after the one being
-  // processed are in flight (units of a wave: wave, wave + W, ...).
-  u32x4_t kbuf[PF + 1][4], vbuf[PF + 1][4];
-#pragma unroll
-  for (int j = 0; j < PF; ++j)
-    if (wave + j * W < units) load_unit(wave + j * W, kbuf[j], vbuf[j]);
-  for (int unit = wave; unit < units; unit += (PF + 1) * W) {
-#pragma unroll
-    for (int j = 0; j <= PF; ++j) {
-      const int cur = unit + j * W;
-      if (cur >= units) break;
-      if (cur + PF * W < units) load_unit(cur + PF * W, kbuf[(j + PF) % (PF + 1)], vbuf[(j + PF) % (PF + 1)]);
-      process(cur, kbuf[j], vbuf[j]);
+          for (int e = 0; e < 8; ++e) acc[h][e] += pb[u][h] * vf[e];
+      }
     }
   }
 

@@ -362,9 +362,9 @@ static int64_t call_workspace(const ftk_plan& p, int epi, bool pro) {
 
 // ---- decode attention: launch planning --------------------------------------
 
-// Workgroups the default split count aims at: two per CU, so the cache rows of
-// a short context are all in flight at once.
-constexpr int kAttnGroupsPerCu = 2;
+// Workgroups the default split count aims at: one per CU (measured on MI355X:
+// 32 intervals per KV head beat 64 at B = 1 from 1K to 32K slots).
+constexpr int kAttnGroupsPerCu = 1;
 
 static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, int cus, const ftk_attn_config* cfg,
                      ftk_attn_plan* p, AttnShape* shape) {
@@ -375,11 +375,11 @@ static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, i
   const int groups = (int)(B * Hkv);
   int kind = cfg && cfg->kind ? cfg->kind : (D == 128 && G <= 4 ? FTK_ATTN_QUAD : FTK_ATTN_ROWS);
   const int waves = cfg && cfg->waves ? cfg->waves : 4;
-  int unroll = cfg && cfg->unroll ? cfg->unroll : (kind == FTK_ATTN_QUAD ? 2 : 4);
+  int unroll = cfg && cfg->unroll ? cfg->unroll : (kind == FTK_ATTN_QUAD ? 1 : 4);
   if (kind == FTK_ATTN_ROWS && !(cfg && cfg->unroll) && !attn_supported(kind, (int)D, (int)G, waves, unroll))
     unroll = 2;
   if (!attn_supported(kind, (int)D, (int)G, waves, unroll)) return FTK_ERR_INVALID;
-  const int64_t unit = kind == FTK_ATTN_QUAD ? 16 : (64 / (D / 8)) * unroll;  // slots one wave takes per step
+  const int64_t unit = kind == FTK_ATTN_QUAD ? 16 * unroll : (64 / (D / 8)) * unroll;  // slots per wave step
   int64_t splits;
   if (cfg && cfg->splits) {
     if (cfg->splits < 1) return FTK_ERR_INVALID;

@@ -157,6 +157,15 @@ __device__ __forceinline__ u32x4_t load_stream16(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
 
+// Raw buffer loads: dword 3 of a gfx9 buffer descriptor for untyped 32-bit data.
+constexpr int kBufferFlags = 0x00020000;
+
+// 16 bytes at byte `offset` of a buffer, streamed (non-temporal). Past the
+// descriptor's range the load returns zeros and does not touch memory.
+__device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 2));
+}
+
 __device__ __forceinline__ u32x4_t load16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }

@@ -227,7 +227,7 @@ typedef struct ftk_attn_config {
   int splits;  /* slot intervals per (row, KV head), at most 1024; 1 = no merge launch */
   int waves;   /* waves per workgroup (4, 8) */
   int unroll;  /* ROWS: cache rows of K (and of V) in flight per lane per step (2, 4, 8);
-                  QUAD: 16-row units a wave has in flight beyond the one it computes (1, 2) */
+                  QUAD: groups of 16 cache rows per wave step, the loads of the next step in flight (1, 2) */
 } ftk_attn_config;
 typedef struct ftk_attn_plan {
   int kind;

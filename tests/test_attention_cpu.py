@@ -32,13 +32,13 @@ def test_intervals_cover_every_slot_once(b, hq, hkv, c, d, splits):
 
 
 def test_default_plan_for_qwen3_8b_decode():
-    """About two workgroups per CU, and at least one load step per wave in every interval."""
+    """About one workgroup per CU, and at least one load step per wave in every interval."""
     p = plan(1, 32, 8, 4096, 128)
-    assert (p.kind, p.splits, p.chunk, p.waves, p.unroll, p.grid) == (_native.ATTN_QUAD, 64, 64, 4, 2, 512)
+    assert (p.kind, p.splits, p.chunk, p.waves, p.unroll, p.grid) == (_native.ATTN_QUAD, 32, 128, 4, 1, 256)
     p = plan(16, 32, 8, 4096, 128)
-    assert (p.splits, p.chunk, p.grid) == (4, 1024, 512)
+    assert (p.splits, p.chunk, p.grid) == (2, 2048, 256)
     for c in (1, 63, 64, 65, 100, 1000):  # short contexts: no more intervals than steps of 4 waves x 16 rows
-        assert plan(1, 32, 8, c, 128).splits == min(64, -(-c // 64))
+        assert plan(1, 32, 8, c, 128).splits == min(32, -(-c // 64))
 
 
 def test_kind_by_head_dim_and_group_size():
@@ -46,7 +46,7 @@ def test_kind_by_head_dim_and_group_size():
     for g in range(1, 9):
         p = plan(1, 8 * g, 8, 1000, 128)
         assert p.kind == (_native.ATTN_QUAD if g <= 4 else _native.ATTN_ROWS)
-        assert p.unroll == (2 if g <= 4 else 4 if g <= 6 else 2)
+        assert p.unroll == (1 if g <= 4 else 4 if g <= 6 else 2)
         assert plan(1, 8 * g, 8, 1000, 64).kind == _native.ATTN_ROWS
     assert plan(1, 64, 8, 1000, 128).unroll == 2  # 8 heads per KV head: fewer rows in flight
 
