@@ -253,6 +253,9 @@ def main():
     ap.add_argument("--profile-gate-up", type=int, default=0, metavar="PASSES",
                     help="profiling mode: only PASSES eager passes of the 36 gate/up + SwiGLU launches, "
                          "then one 1 GiB device copy as the counter reference")
+    ap.add_argument("--profile-attention", type=int, default=0, metavar="PASSES",
+                    help="profiling mode: PASSES eager passes of decode attention over each ATTN_CASES cache set "
+                         "(distinct caches), then one 1 GiB device copy as the counter reference")
     ap.add_argument("--profile-rows", type=str, default="", metavar="M[,M...]",
                     help="profiling mode: two eager passes of the 36-layer projection chain at each M rows "
                          "(the C4 workload), then one 1 GiB device copy as the counter reference")
@@ -273,6 +276,9 @@ def main():
         return
     if args.profile_rows:
         profile_rows(cfg, dev, [int(m) for m in args.profile_rows.split(",")])
+        return
+    if args.profile_attention:
+        profile_attention(cfg, dev, args.profile_attention)
         return
     model = Model(cfg, dev)
     stage("Qwen3-8B weights resident")
@@ -430,6 +436,28 @@ def shapes_table(model8, step8, dev):
 #: Decode attention next to the projections (Qwen3-8B heads: 32 query, 8 KV, D = 128):
 #: (rows, cache slots, distinct caches timed in one graph: together over the 256 MB MALL).
 ATTN_CASES = ((1, 4096, 36), (1, 32768, 8), (16, 4096, 4))
+
+
+def profile_attention(cfg, dev, passes):
+    """Eager decode-attention launches over every ATTN_CASES cache set (for rocprofv3), then a 1 GiB copy."""
+    hq, hkv, d = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
+    for b, c, copies in ATTN_CASES:
+        g = torch.Generator(device=dev).manual_seed(11)
+        ks = [torch.randn((b, hkv, c, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+        vs = [torch.randn((b, hkv, c, d), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+        q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.bfloat16)
+        pos = torch.tensor([c - 1], device=dev, dtype=torch.int64)
+        for _ in range(passes):
+            for k, v in zip(ks, vs):
+                DA.decode_attention(q, k, v, pos, d ** -0.5)
+        torch.cuda.synchronize()
+        stage(f"attention B={b} C={c}: {passes} passes over {copies} caches")
+        del ks, vs
+    src = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    stage("1 GiB reference copy done")
 
 
 def attention_table(cfg, dev):
