@@ -397,10 +397,13 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
 
 // out[q] = bf16( sum_s acc_s exp2(m_s - M) / sum_s l_s exp2(m_s - M) ), M = max_s m_s,
 // for one query head q = group * G + h per workgroup (engine/kernels/decode_attention.py:102-128).
-// The splits' weights are formed once, in parallel, into LDS; then each wave
-// sums the numerators of every kMergeWaves-th split over its lanes' dimensions
-// and the wave totals are added in wave order.
+// One memory round trip for up to kMergeWaves * kMergePre splits: each thread
+// loads one split's (max, denominator) and each wave the numerators of its
+// first kMergePre splits (s = wave + kMergeWaves i) before anything waits.
+// The weights are then formed in parallel into LDS, and the wave totals are
+// added in wave order.
 constexpr int kMergeWaves = 4;
+constexpr int kMergePre = 8;
 
 template <int D>
 __global__ __launch_bounds__(64 * kMergeWaves) void attn_merge_kernel(const float* partial, const float* stats,
@@ -415,8 +418,18 @@ __global__ __launch_bounds__(64 * kMergeWaves) void attn_merge_kernel(const floa
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   auto slot = [&](int s) { return ((size_t)group * splits + s) * groups_per_kv + h; };
 
-  float top = -INFINITY;
-  for (int s = t; s < splits; s += T) top = fmaxf(top, stats[slot(s) * 2]);
+  f32x2_t st = {-INFINITY, 0.f};
+  if (t < splits) st = *reinterpret_cast<const f32x2_t*>(stats + slot(t) * 2);
+  float pre[kMergePre][E];
+#pragma unroll
+  for (int i = 0; i < kMergePre; ++i) {
+    const int s = wave + kMergeWaves * i;
+#pragma unroll
+    for (int e = 0; e < E; ++e) pre[i][e] = s < splits ? partial[slot(s) * D + lane * E + e] : 0.f;
+  }
+
+  float top = st[0];
+  for (int s = t + T; s < splits; s += T) top = fmaxf(top, stats[slot(s) * 2]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) top = fmaxf(top, __shfl_xor(top, off));
   if (lane == 0) red[wave] = top;
@@ -427,7 +440,12 @@ __global__ __launch_bounds__(64 * kMergeWaves) void attn_merge_kernel(const floa
   __syncthreads();
 
   float den = 0.f;
-  for (int s = t; s < splits; s += T) {
+  if (t < splits) {
+    const float c = st[0] == -INFINITY ? 0.f : exp2_f32(st[0] - top);
+    weight[t] = c;
+    den = st[1] * c;
+  }
+  for (int s = t + T; s < splits; s += T) {
     const float ms = stats[slot(s) * 2];
     const float c = ms == -INFINITY ? 0.f : exp2_f32(ms - top);
     weight[s] = c;
@@ -441,8 +459,15 @@ __global__ __launch_bounds__(64 * kMergeWaves) void attn_merge_kernel(const floa
   float num[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) num[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMergePre; ++i) {
+    const int s = wave + kMergeWaves * i;
+    const float c = s < splits ? weight[s] : 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) num[e] += pre[i][e] * c;
+  }
 #pragma unroll 4
-  for (int s = wave; s < splits; s += kMergeWaves) {
+  for (int s = wave + kMergeWaves * kMergePre; s < splits; s += kMergeWaves) {
     const float c = weight[s];
 #pragma unroll
     for (int e = 0; e < E; ++e) num[e] += partial[slot(s) * D + lane * E + e] * c;
