@@ -766,6 +766,50 @@ int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const
   return hip_status(launch_attention(a, shape, reinterpret_cast<hipStream_t>(stream)));
 }
 
+int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride, const void* q_gain,
+                           const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+                           int64_t table_rows, const int64_t* position, const int64_t* phases, void* query,
+                           void* keys, void* values, int64_t batch, int64_t tokens, int64_t q_heads,
+                           int64_t kv_heads, int64_t capacity, int64_t dim, int mode, void* stream) {
+  if (!packed || !q_gain || !k_gain || !cos || !sin || !query || !keys || !values) return FTK_ERR_INVALID;
+  if (batch < 1 || tokens < 1 || q_heads < 1 || kv_heads < 1 || capacity < 1 || table_rows < 1 || splits < 1)
+    return FTK_ERR_INVALID;
+  if (mode & ~(FTK_ROPE_PREFILL | FTK_ROPE_ROWS | FTK_ROPE_TABLE)) return FTK_ERR_INVALID;
+  if ((mode & FTK_ROPE_PREFILL) && (mode & FTK_ROPE_ROWS)) return FTK_ERR_INVALID;
+  if ((mode & FTK_ROPE_TABLE) && (!(mode & FTK_ROPE_ROWS) || !phases)) return FTK_ERR_INVALID;
+  if (!(mode & FTK_ROPE_PREFILL) && !position) return FTK_ERR_INVALID;
+  if (tokens > capacity || splits > 1 && split_stride < batch * tokens * (q_heads + 2 * kv_heads) * dim)
+    return FTK_ERR_INVALID;
+  if (dim != 64 && dim != 128) return FTK_ERR_UNSUPPORTED;
+  if (batch * tokens > INT32_MAX / 2 || q_heads + kv_heads > 65535 * 4 || capacity > INT32_MAX) return FTK_ERR_INVALID;
+  const void* ptrs[] = {packed, q_gain, k_gain, cos, sin, query, keys, values};
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) & 3u) return FTK_ERR_UNSUPPORTED;
+  RopeArgs a;
+  a.packed = packed;
+  a.splits = splits;
+  a.split_stride = split_stride;
+  a.q_gain = (const uint16_t*)q_gain;
+  a.k_gain = (const uint16_t*)k_gain;
+  a.q_eps = q_eps;
+  a.k_eps = k_eps;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.table_rows = table_rows;
+  a.position = position;
+  a.phases = phases;
+  a.query = (uint16_t*)query;
+  a.keys = (uint16_t*)keys;
+  a.values = (uint16_t*)values;
+  a.tokens = (int)tokens;
+  a.q_heads = (int)q_heads;
+  a.kv_heads = (int)kv_heads;
+  a.capacity = (int)capacity;
+  a.dim = (int)dim;
+  a.mode = mode;
+  return hip_status(launch_qk_rope(a, (int)(batch * tokens), reinterpret_cast<hipStream_t>(stream)));
+}
+
 int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream) {
   if (!partial || !out || splits < 1 || count < 1 || splits > INT32_MAX) return FTK_ERR_INVALID;
   if (count > (int64_t)UINT32_MAX * kThreads) return FTK_ERR_INVALID;

@@ -156,6 +156,26 @@ constexpr int kAttnMaxSplits = 1024;  // slot intervals per group the merge kern
 bool attn_supported(int kind, int dim, int group_size, int waves, int unroll);
 hipError_t launch_attention(const AttnArgs& a, const AttnShape& s, hipStream_t stream);
 
+// Arguments of one Q/K head RMSNorm + RoPE + KV-cache update (engine/kernels/qk_rope.py:13-94).
+struct RopeArgs {
+  const void* packed;        // BF16 [rows, (Hq + 2 Hkv) D], or FP32 partials [splits][rows * (Hq + 2 Hkv) D]
+  int splits;                // 1: BF16 input
+  int64_t split_stride;      // elements between partial planes (splits > 1)
+  const uint16_t* q_gain;    // [D] q_norm weight
+  const uint16_t* k_gain;    // [D] k_norm weight
+  float q_eps, k_eps;
+  const uint16_t* cos;       // [table_rows, D] BF16
+  const uint16_t* sin;
+  int64_t table_rows;
+  const int64_t* position;   // [1], [B] (rows) or the prefill positions (unused)
+  const int64_t* phases;     // [rows] with FTK_ROPE_TABLE, else null
+  uint16_t* query;           // [rows, Hq, D]
+  uint16_t* keys;            // [B, Hkv, C, D]
+  uint16_t* values;
+  int tokens, q_heads, kv_heads, capacity, dim, mode;
+};
+hipError_t launch_qk_rope(const RopeArgs& a, int rows, hipStream_t stream);
+
 // Greedy-argmax second stage: ids[m] (and top[m]) from keys[slot * M + m], slot < slots.
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream);

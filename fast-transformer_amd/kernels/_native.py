@@ -19,6 +19,7 @@ EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
 PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
 KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE = range(8)
 ATTN_AUTO, ATTN_ROWS, ATTN_QUAD = range(3)
+ROPE_PREFILL, ROPE_ROWS, ROPE_TABLE = 0x1, 0x2, 0x4
 MAX_ROWS = 32
 
 _c_void_p, _i64, _int, _float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -101,6 +102,9 @@ SIGNATURES = {
     "ftk_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(AttnConfig)]),
     "ftk_plan_decode_attention": (_int, [_i64, _i64, _i64, _i64, _i64, _int, ctypes.POINTER(AttnConfig),
                                          ctypes.POINTER(AttnPlan)]),
+    "ftk_qk_rope_cache_bf16": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _float, _float, _c_void_p,
+                                      _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
     "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
                                  ctypes.POINTER(_i64)]),

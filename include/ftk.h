@@ -255,6 +255,26 @@ int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const
 /* Workspace bytes of that call on the current device (-1: invalid shape or no device). */
 int64_t ftk_decode_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
                                              int64_t dim, const ftk_attn_config* cfg);
+/* ---- Q/K head norm + RoPE + KV-cache update ---------------------------------------- */
+#define FTK_ROPE_PREFILL 0x1  /* token t goes to cache slot t (else position + t) */
+#define FTK_ROPE_ROWS 0x2     /* one position per batch row; cos/sin [B, T, D] (else [1, T, D] shared) */
+#define FTK_ROPE_TABLE 0x4    /* cos/sin are whole [table_rows, D] tables; row b token t rotates at
+                                 position[b] + phases[b, t] (needs FTK_ROPE_ROWS) */
+/* For each row b (of `batch`), token t (of `tokens`) and head h of the packed QKV
+ * [B, T, (Hq + 2 Hkv) D] (BF16, or `splits` > 1 FP32 partial planes `split_stride`
+ * elements apart, summed and rounded to BF16): n = bf16(x / sqrt(mean(x^2) + eps)),
+ * w = bf16(n * gain) with q_gain / q_eps for the Hq query heads and k_gain / k_eps
+ * for the Hkv key heads, then out = bf16(bf16(w * cos) + bf16(rotate_half(w) * sin)).
+ * Query heads go to query [B, T, Hq, D]; key heads to keys [B, Hkv, C, D] at the
+ * step's slot, and the value heads are copied to values at the same slot. Slots
+ * outside [0, capacity) and phases outside [0, table_rows) are skipped on the
+ * device. D is 64 or 128; pointers 4-byte aligned. Replaces qk_rope_cache
+ * (engine/kernels/qk_rope.py:13-129). */
+int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride, const void* q_gain,
+                           const void* k_gain, float q_eps, float k_eps, const void* cos, const void* sin,
+                           int64_t table_rows, const int64_t* position, const int64_t* phases, void* query,
+                           void* keys, void* values, int64_t batch, int64_t tokens, int64_t q_heads,
+                           int64_t kv_heads, int64_t capacity, int64_t dim, int mode, void* stream);
 /* ---- planning (host only, no device needed) ---------------------------------- */
 /* The launch ftk_decode_attention_bf16 would make on `compute_units` CUs. */
 int ftk_plan_decode_attention(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity, int64_t dim,
