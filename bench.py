@@ -36,6 +36,7 @@ from kernels import _native  # noqa: E402
 from kernels import argmax as A  # noqa: E402
 from kernels import decode_attention as DA  # noqa: E402
 from kernels import linear as L  # noqa: E402
+from kernels import qk_rope as R  # noqa: E402
 from kernels import swiglu as S  # noqa: E402
 
 METRIC = "M=1 bf16 GEMV HBM GB/s (% of peak) + µs/decode-layer, Qwen3-8B shapes"
@@ -320,6 +321,7 @@ def main():
     if not args.no_shapes:
         per_shape = shapes_table(model, step, dev)
         per_shape.update(attention_table(cfg, dev))
+        per_shape.update(full_layer_table(model, dev))
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -458,6 +460,56 @@ def profile_attention(cfg, dev, passes):
     dst.copy_(src)
     torch.cuda.synchronize()
     stage("1 GiB reference copy done")
+
+
+class _Norm:
+    """The q_norm / k_norm interface qk_rope_cache reads: .weight and .variance_epsilon."""
+
+    def __init__(self, weight, eps):
+        self.weight, self.variance_epsilon = weight, eps
+
+
+#: Cache slots of the full decode layer (every layer's cache distinct; 604 MB for 36 layers).
+FULL_LAYER_CONTEXT = 4096
+
+
+def full_layer_table(model, dev):
+    """One whole M=1 decode layer on this library, per layer of the 36, at a 4K-slot cache:
+    residual-add norm + QKV, QK norm + RoPE + cache write, decode attention, O, residual-add
+    norm + gate/up + SwiGLU, down (engine/decode.py:229-261, engine/layers.py:32-90)."""
+    cfg = model.cfg
+    hq, hkv, d, c = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"], FULL_LAYER_CONTEXT
+    g = torch.Generator(device=dev).manual_seed(13)
+    caches = [(torch.randn((1, hkv, c, d), generator=g, device=dev).to(torch.bfloat16),
+               torch.randn((1, hkv, c, d), generator=g, device=dev).to(torch.bfloat16)) for _ in model.layers]
+    norms = [(_Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS),
+              _Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS))
+             for _ in model.layers]
+    angle = (c - 1) / 1_000_000.0 ** (torch.arange(0, d, 2, device=dev, dtype=torch.float64) / d)
+    cos = torch.cat([angle, angle]).cos().to(torch.bfloat16).reshape(1, 1, d)
+    sin = torch.cat([angle, angle]).sin().to(torch.bfloat16).reshape(1, 1, d)
+    pos = torch.tensor([c - 1], device=dev, dtype=torch.int64)
+    hidden = torch.randn((1, cfg["hidden"]), generator=g, device=dev).to(torch.bfloat16)
+    resid = torch.randn((1, cfg["hidden"]), generator=g, device=dev).to(torch.bfloat16)
+
+    def layers():
+        h, r = hidden, resid
+        for lw, (k, v), (qn, kn) in zip(model.layers, caches, norms):
+            qkv, r = L.add_rms_norm_linear(h, r, lw["ln1"], EPS, lw["qkv"])
+            q = R.qk_rope_cache(qkv.view(1, 1, -1), qn, kn, cos, sin, pos, k, v, hq)
+            attn = DA.decode_attention(q, k, v, pos, d ** -0.5)
+            o = L.linear(attn.reshape(1, hq * d), lw["o"])
+            act, r = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS, residual=r)
+            h = L.linear(act, lw["down"])
+        return h, r
+
+    graph = capture(layers)
+    us = time_graph(graph, reps=5) / len(model.layers)
+    lb = layer_bytes(cfg, 1)
+    byts = sum(lb.values()) + 4 * 2 * cfg["hidden"] + 2 * hkv * c * d * 2
+    del caches, graph
+    stage("full decode layer done")
+    return {f"C3 8B full decode layer M=1 (attention over {c} slots)": shape_entry(us, byts)}
 
 
 def attention_table(cfg, dev):

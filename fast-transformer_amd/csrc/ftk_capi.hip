@@ -780,6 +780,8 @@ int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride,
   if (!(mode & FTK_ROPE_PREFILL) && !position) return FTK_ERR_INVALID;
   if (tokens > capacity || splits > 1 && split_stride < batch * tokens * (q_heads + 2 * kv_heads) * dim)
     return FTK_ERR_INVALID;
+  if (!(mode & FTK_ROPE_TABLE) && table_rows < ((mode & FTK_ROPE_ROWS) ? batch * tokens : tokens))
+    return FTK_ERR_INVALID;  // shared [1, T, D] or per-row [B, T, D] rows must cover every phase
   if (dim != 64 && dim != 128) return FTK_ERR_UNSUPPORTED;
   if (batch * tokens > INT32_MAX / 2 || q_heads + kv_heads > 65535 * 4 || capacity > INT32_MAX) return FTK_ERR_INVALID;
   const void* ptrs[] = {packed, q_gain, k_gain, cos, sin, query, keys, values};

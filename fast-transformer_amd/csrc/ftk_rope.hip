@@ -7,9 +7,9 @@
 // FP32 with the reference's roundings: n = bf16(x inv_std), w = bf16(n gain),
 // out = bf16(bf16(w cos) + bf16(rot sin)). Query heads go to the token-major
 // query [rows, Hq, D]; key heads and the copied value heads to the caches
-// [B, Hkv, C, D] at the step's slot. Slots outside the cache and phases outside
-// the cos/sin tables (device-side values the host cannot check) are skipped:
-// nothing is read or written out of bounds.
+// [B, Hkv, C, D] at the step's slot. Slots outside the cache and table phases
+// outside the cos/sin tables (device-side values the host cannot check) are
+// skipped: nothing is read or written out of bounds.
 #include "../../include/ftk.h"
 #include "ftk_internal.h"
 
@@ -71,26 +71,38 @@ __global__ __launch_bounds__(64 * W) void qk_rope_kernel(RopeArgs a) {
   const int64_t np = (int64_t)(a.q_heads + 2 * a.kv_heads) * D;
   const bool is_q = head < a.q_heads;
 
+  // Every load that does not depend on the device-side position goes out first
+  // (one memory round trip); with shared or per-row cos/sin rows the phase is
+  // the token or the row, checked against the tables on the host.
+  const bool table = (a.mode & FTK_ROPE_TABLE) != 0;
+  const int64_t vat = r * np + (int64_t)(a.q_heads + a.kv_heads + (head - a.q_heads)) * D + col;
+  float x[E], g[E], c[E], s[E];
+  uint32_t vbits = 0;
+  load_merged<E>(a, r * np + (int64_t)head * D + col, x);
+  load_table<E>((is_q ? a.q_gain : a.k_gain) + col, g);
+  if (!is_q && a.splits == 1) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.packed) + vat;
+    vbits = E == 2 ? *reinterpret_cast<const uint32_t*>(src) : (uint32_t)*src;
+  }
   int64_t phase = (a.mode & FTK_ROPE_ROWS) ? r : t;
-  if (a.mode & FTK_ROPE_TABLE) phase = a.position[b] + a.phases[r];
+  if (!table) {
+    load_table<E>(a.cos + phase * D + col, c);
+    load_table<E>(a.sin + phase * D + col, s);
+  }
   int64_t slot = 0;
   if (!is_q) slot = (a.mode & FTK_ROPE_PREFILL) ? t : a.position[(a.mode & FTK_ROPE_ROWS) ? b : 0] + t;
-  if (phase < 0 || phase >= a.table_rows) return;
-  if (!is_q && (slot < 0 || slot >= a.capacity)) return;
+  if (table) {
+    phase = a.position[b] + a.phases[r];
+    if (phase < 0 || phase >= a.table_rows) return;  // wave-uniform; no barrier in this kernel
+    load_table<E>(a.cos + phase * D + col, c);
+    load_table<E>(a.sin + phase * D + col, s);
+  }
 
-  float x[E];
-  load_merged<E>(a, r * np + (int64_t)head * D + col, x);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) ss += x[e] * x[e];
   ss = wave_sum(ss);
   const float inv_std = 1.0f / sqrtf(ss / (float)D + (is_q ? a.q_eps : a.k_eps));
-  const uint16_t* gain = is_q ? a.q_gain : a.k_gain;
-  float g[E], c[E], s[E];
-  load_table<E>(gain + col, g);
-  load_table<E>(a.cos + phase * D + col, c);
-  load_table<E>(a.sin + phase * D + col, s);
-
   float w[E], out[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) w[e] = round_bf16(round_bf16(x[e] * inv_std) * g[e]);
@@ -104,16 +116,15 @@ __global__ __launch_bounds__(64 * W) void qk_rope_kernel(RopeArgs a) {
     store_bf16<E>(a.query + ((int64_t)r * a.q_heads + head) * D + col, out);
     return;
   }
+  if (slot < 0 || slot >= a.capacity) return;
   const int kv = head - a.q_heads;
   const int64_t at = (((int64_t)b * a.kv_heads + kv) * a.capacity + slot) * D + col;
   store_bf16<E>(a.keys + at, out);
-  const int64_t vat = r * np + (int64_t)(a.q_heads + a.kv_heads + kv) * D + col;
   if (a.splits == 1) {  // the value head as it is, bit for bit
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(a.packed) + vat;
     if constexpr (E == 2) {
-      *reinterpret_cast<uint32_t*>(a.values + at) = *reinterpret_cast<const uint32_t*>(src);
+      *reinterpret_cast<uint32_t*>(a.values + at) = vbits;
     } else {
-      a.values[at] = *src;
+      a.values[at] = (uint16_t)vbits;
     }
   } else {
     float v[E];

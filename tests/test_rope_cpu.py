@@ -33,6 +33,7 @@ def test_c_abi_rejects_before_launch():
     assert status(mode=_native.ROPE_TABLE | _native.ROPE_ROWS) == _native.FTK_ERR_INVALID  # ... and phases
     assert status(tokens=17, cap=16) == _native.FTK_ERR_INVALID
     assert status(splits=2, stride=10) == _native.FTK_ERR_INVALID
+    assert status(tokens=17, cap=32) == _native.FTK_ERR_INVALID  # 16 table rows for 17 tokens
     assert status(dim=96) == _native.FTK_ERR_UNSUPPORTED
     assert status(ptr=ctypes.c_void_p(66)) == _native.FTK_ERR_UNSUPPORTED  # 4-byte alignment
 
