@@ -51,7 +51,7 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     _native.require_gpu(x, weight, norm_weight, top, residual)
     if residual is not None and norm_weight is None:
         raise ValueError("a residual needs the norm it feeds (norm_weight)")
-    from kernels.linear import fused_project, linear
+    from kernels.linear import fused_project, linear, prefer_native
     from kernels.rmsnorm import add_rms_norm, rms_norm
 
     shape = x.shape
@@ -63,8 +63,9 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < m):
         raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
-    status = fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
-                           config=config)
+    status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
+        fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
+                      config=config)
     if status != _native.FTK_OK:
         if residual is not None:
             xn = add_rms_norm(x, residual, norm_weight, eps)[0]

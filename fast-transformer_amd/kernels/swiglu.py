@@ -39,7 +39,7 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
     _native.require_gpu(x, gate_up_weight, norm_weight, residual)
     if residual is not None and norm_weight is None:
         raise ValueError("a residual needs the norm it feeds (norm_weight)")
-    from kernels.linear import fused_project, linear
+    from kernels.linear import fused_project, linear, prefer_native
 
     shape = x.shape
     flat = x.reshape(-1, shape[-1]).contiguous()
@@ -50,8 +50,9 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
     out = torch.empty((m, n // 2), device=x.device, dtype=torch.bfloat16)
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
     summed = None if residual is None else torch.empty_like(res)
-    status = fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
-                           summed=summed, config=config)
+    status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
+        fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
+                      summed=summed, config=config)
     if status != _native.FTK_OK:
         from kernels.rmsnorm import add_rms_norm, rms_norm
         if residual is not None:

@@ -125,6 +125,28 @@ def test_more_rows_match_oracle(cuda, m):
     assert within(bf16.to_f32(to_bits(got)), bf16.to_f32(want))
 
 
+@pytest.mark.parametrize("m", [17, 24, 32])
+def test_rows_past_sixteen_default_to_the_native_gemm(cuda, m):
+    """From 17 rows the default is torch's GEMM (measured faster there), as the reference keeps cuBLAS
+    unless a timed kind beats it; the fused forms run their norm / epilogue kernels around it."""
+    from kernels import swiglu as S
+    from kernels.rmsnorm import rms_norm
+    k, n = 1024, 1536
+    x = seeded((m, k), seed=40 + m, device=cuda)
+    w = seeded((n, k), seed=41, scale=0.02, device=cuda)
+    g = seeded((k,), seed=42, scale=0.1, shift=1.0, device=cuda)
+    assert torch.equal(L.linear(x, w), F.linear(x, w))
+    normed = L.rms_norm_linear(x, g, 1e-6, w)
+    assert torch.equal(normed, F.linear(rms_norm(x, g, 1e-6), w))
+    assert within(bf16.to_f32(to_bits(normed)), bf16.to_f32(path.norm_project(to_bits(x), to_bits(g), 1e-6,
+                                                                               to_bits(w))))
+    act = S.gate_up_swiglu(x, w, g, 1e-6)
+    assert torch.equal(act, S.swiglu(F.linear(rms_norm(x, g, 1e-6), w)))
+    # an explicit launch choice still runs this library's kernel
+    assert within(bf16.to_f32(to_bits(L.project(x, w, _native.Config(_native.KIND_MFMA, 0, 0, 0, 0)))),
+                  bf16.to_f32(path.project(to_bits(x), to_bits(w))))
+
+
 def test_linear_keeps_reference_signature_and_fallbacks(cuda):
     x = seeded((2, 3, 256), seed=13, device=cuda)
     w = seeded((512, 256), seed=14, scale=0.02, device=cuda)

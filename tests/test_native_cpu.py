@@ -322,3 +322,10 @@ def test_default_kind_for_8b_shapes():
     p = _native.Plan()
     _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
     assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
+
+
+def test_native_gemm_from_seventeen_rows_without_a_config():
+    from kernels import linear as L
+    assert L.NATIVE_FROM_ROWS == 17
+    assert not L.prefer_native(16) and L.prefer_native(17) and L.prefer_native(32)
+    assert not L.prefer_native(32, _native.Config(_native.KIND_MFMA, 0, 0, 0, 0))
