@@ -158,7 +158,9 @@ struct StageDefault {
 static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
   if (M < 1 || M > kStageMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
   const int t = epi == FTK_EPI_SWIGLU ? 2 : 1;
-  const int u = quad_segments((int)K, 8) > 4 ? 3 : epi == FTK_EPI_ARGMAX ? 4 : 2;
+  // Segments in flight per wave: 3 for the long K (x streamed beside the
+  // weights), else 2 (lm_head + argmax at 5 rows: 208 us against 220 with 4).
+  const int u = quad_segments((int)K, 8) > 4 ? 3 : 2;
   const StageDefault order[] = {{t, 8, u}, {t, 8, 2}, {t, 8, 4}, {t, 8, 3}};
   for (const StageDefault& d : order)
     if (stage_supported((int)M, d.t, (int)K, d.kw, d.unroll, epi, pro)) return d;
