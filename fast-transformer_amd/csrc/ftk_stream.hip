@@ -91,13 +91,19 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     // Sum of squares in the thread order of the other kinds' prologues
     // (thread t < 256: chunks t, t + 256, ...), so every kind scales a row
     // alike. With KW = W = 4 thread t's own chunks (4 j + wave) 64 + lane are
-    // exactly those, in that order; otherwise the first 4 waves re-read x.
+    // exactly those, in that order. With one chunk per lane (C = 1) and
+    // KW <= 4, the first row group's thread t holds chunk t and every chunk
+    // is below 64 KW, so the other threads add nothing. Otherwise the first
+    // 4 waves re-read x (after the weight window: those loads wait for it).
+    constexpr bool kOwnChunks = (KW == kWaves && W == kWaves) || (C == 1 && KW <= kWaves);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       float ss = 0.f;
-      if constexpr (KW == kWaves && W == kWaves) {
+      if constexpr (kOwnChunks) {
+        if (grp == 0) {
 #pragma unroll
-        for (int j = 0; j < C; ++j) ss = sum_squares8(xr[m][j], ss);
+          for (int j = 0; j < C; ++j) ss = sum_squares8(xr[m][j], ss);
+        }
       } else {
         const int KC = K >> 3;
         if (m < M && tid < kThreads)
