@@ -73,10 +73,15 @@ struct StreamDefault {
 };
 static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
   if (M < 1 || M > kStreamMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
-  for (int kw : {4, 2, 1, 8}) {
+  // Rows longer than 8192 (down, K = 12288) split K over 8 waves (M = 1 down:
+  // 16.25 us against 17.0 with 4); otherwise 4 waves first.
+  const int order_long[] = {8, 4, 2, 1}, order[] = {4, 2, 1, 8};
+  for (int kw : (K > 8192 ? order_long : order)) {
     const int c = stream_chunks((int)K, kw);
     if (c == 0) continue;
-    const int want = (c <= 2 && gemv_outputs(epi, (int)N) >= 6144) ? 4 : 2;
+    // 4 rows per tile for the wide outputs (gate/up's 12288, lm_head), else 2
+    // (QKV's 6144: 9.28 us against 9.51 with 4).
+    const int want = (c <= 2 && gemv_outputs(epi, (int)N) > 6144) ? 4 : 2;
     for (int rpw : {want, 2, 4, 8})
       if (stream_supported((int)M, rpw, (int)K, kw, epi)) return {rpw, kw};
   }
@@ -87,8 +92,12 @@ static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
 // tile per workgroup, the largest (lm_head) as deep walks of kStreamMaxTiles.
 // Rows of at most 1024 elements (Qwen3-0.6B's QKV and gate/up) take two tiles
 // per workgroup (0.6B gate/up + SwiGLU: 4.70 -> 4.45 us).
-static int64_t stream_default_cap(int tiles, int cus, int64_t K) {
+static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K) {
   if (K <= 1024 && tiles <= 4096) return tiles / 2 > 2LL * cus ? tiles / 2 : 2LL * cus;
+  // Long rows (down, K = 12288): at M = 1 one tile per workgroup; with more x
+  // rows one workgroup per CU walking tiles (M = 2..4: 16.9-17.9 us, against
+  // 19.6-22.1 with one tile each).
+  if (K > 8192 && tiles <= 4096) return M == 1 ? tiles : cus;
   if (tiles <= 4096) return 2LL * cus;
   if (tiles <= 16384) return 32LL * cus;
   return 0;  // the depth limit sets the grid
@@ -265,7 +274,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // Fewest workgroups that keep every walk at the same depth, and no deeper than
     // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
-                                                  : stream_default_cap(p->tiles, cus, K);
+                                                  : stream_default_cap(p->tiles, cus, M, K);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
