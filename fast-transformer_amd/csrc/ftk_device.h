@@ -152,9 +152,16 @@ __device__ __forceinline__ f32x4_t mfma4x4x4(uint32_t a0, uint32_t a1, uint32_t 
                                                 0, 0, 0);
 }
 
+// Every pointer these loads take is global memory (a kernel argument plus an
+// offset). Saying so keeps them global_load: through a generic pointer that the
+// compiler cannot trace to an argument (one carried across loop iterations) it
+// emits flat_load, which also counts in lgkmcnt, so every LDS wait after it
+// would wait for the memory load too and empty the load window.
+typedef __attribute__((address_space(1))) const u32x4_t global_u32x4_t;
+
 // Streaming 16-byte load: weights are read exactly once per call.
 __device__ __forceinline__ u32x4_t load_stream16(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return __builtin_nontemporal_load((global_u32x4_t*)p);
 }
 
 // Raw buffer loads: dword 3 of a gfx9 buffer descriptor for untyped 32-bit data.
@@ -167,7 +174,7 @@ __device__ __forceinline__ u32x4_t buffer_load16(__amdgpu_buffer_rsrc_t rsrc, ui
 }
 
 __device__ __forceinline__ u32x4_t load16(const void* p) {
-  return *reinterpret_cast<const u32x4_t*>(p);
+  return *(global_u32x4_t*)p;
 }
 
 // DPP lane exchange: lanes whose row is masked off read 0.
