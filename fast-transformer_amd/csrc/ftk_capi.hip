@@ -79,9 +79,10 @@ static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
   for (int kw : (K > 8192 ? order_long : order)) {
     const int c = stream_chunks((int)K, kw);
     if (c == 0) continue;
-    // 4 rows per tile for the wide outputs (gate/up's 12288, lm_head), else 2
-    // (QKV's 6144: 9.28 us against 9.51 with 4).
-    const int want = (c <= 2 && gemv_outputs(epi, (int)N) > 6144) ? 4 : 2;
+    // 4 rows per tile for gate/up's 12288 outputs (29.6 us against 31.3 with 2),
+    // else 2 (QKV's 6144: 9.28 us against 9.51 with 4; lm_head + argmax at
+    // M = 1: 192.6 us against 194.8 with 4).
+    const int want = (c <= 2 && epi != FTK_EPI_ARGMAX && gemv_outputs(epi, (int)N) > 6144) ? 4 : 2;
     for (int rpw : {want, 2, 4, 8})
       if (stream_supported((int)M, rpw, (int)K, kw, epi)) return {rpw, kw};
   }
@@ -99,7 +100,9 @@ static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K) {
   // 19.6-22.1 with one tile each).
   if (K > 8192 && tiles <= 4096) return M == 1 ? tiles : cus;
   if (tiles <= 4096) return 2LL * cus;
-  if (tiles <= 16384) return 32LL * cus;
+  // One tile per workgroup at M = 1; from two x rows three tiles per workgroup
+  // (gate/up + SwiGLU at M = 2: 31.0 us against 32.5 with one).
+  if (tiles <= 16384) return M == 1 ? 32LL * cus : 8LL * cus;
   return 0;  // the depth limit sets the grid
 }
 
@@ -316,10 +319,10 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->waves = kw;
     p->threads = 64 * kw;
     p->tiles = mfma_tiles(epi, (int)N, t);
-    const int64_t cap = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
-    const int depth = stage_max_depth(t, kw);
-    const int64_t floor = (p->tiles + depth - 1) / depth;
-    const int64_t units = cap > floor ? cap : floor;
+    // One workgroup per CU (the LDS of one fills most of a CU), each walking its
+    // share of the tiles: lm_head + argmax at 5 rows no longer runs a partial
+    // last round of workgroups.
+    const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     return FTK_OK;
@@ -503,8 +506,8 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
     // Workgroup b walks tiles b + i grid; a tile is T subtiles of 16 weight rows.
     const int t = p->rows_per_wave / 16;
     if (t < 1 || p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
-    const int depth = p->kind == FTK_KIND_STAGE ? stage_max_depth(t, p->waves) : mstream_max_depth(t, p->waves);
-    if ((p->tiles + p->grid - 1) / p->grid > depth) return FTK_ERR_INVALID;
+    if (p->kind == FTK_KIND_MFMA_STREAM && (p->tiles + p->grid - 1) / p->grid > mstream_max_depth(t, p->waves))
+      return FTK_ERR_INVALID;
     const int per = mfma_out_per_tile(epilogue, t);
     for (int b = 0; b < p->grid; ++b)
       for (int tile = b; tile < p->tiles; tile += p->grid) {

@@ -104,7 +104,7 @@ struct StageShape {
   int subtiles;  // T: 16-row MFMA subtiles per tile
   int unroll;    // U: K segments of weight loads in flight per wave
   int kw;        // waves per workgroup, splitting K
-  int grid;      // workgroups; each walks <= stage_max_depth(T, KW) tiles
+  int grid;      // workgroups; each walks tiles wg, wg + grid, ...
   int tiles;
 };
 bool stage_supported(int M, int t, int K, int kw, int unroll, int epi, bool pro);

@@ -147,8 +147,9 @@ constexpr bool quad_fits(int mq, int rs, int c, int kw, bool pro) {
 // ---- M = 5..16 with K = 128 C KW: the STAGE kind (16x16x32 MFMA via LDS) -----
 // Tiles, subtiles and weight rows as the MFMA kind (mfma_weight_row /
 // mfma_tiles), segments as the QUAD kind: wave kw of a workgroup reads the
-// 128-wide K segments j KW + kw. Workgroup b walks tiles b, b + grid, ... (at
-// most stage_max_depth(T, KW): their per-wave partials wait in 64 KiB of LDS).
+// 128-wide K segments j KW + kw. Workgroup b walks tiles b, b + grid, ...; the
+// per-wave partials of up to stage_max_depth(T, KW) of them wait in 64 KiB of
+// LDS before their epilogue runs.
 constexpr int kStageMaxRows = 16;
 FTK_HD constexpr int stage_max_depth(int t, int kw) { return (64 * 1024) / (t * kw * 1024); }
 

@@ -30,9 +30,12 @@
 //     first (sums of squares, one barrier), and each K segment of the slice is
 //     normalised in the first tile right before its MFMAs, with the gain read
 //     from LDS: that VALU work overlaps the weight stream instead of delaying it.
-//   * Per-tile 16 x 16 partials wait in LDS; one barrier at the end, then the
-//     workgroup sums the KW partials in wave order (deterministic) and runs the
-//     epilogue on every output of its tiles.
+//   * Per-tile 16 x 16 partials wait in LDS. After every DMAX tiles of the walk
+//     (and after the last) a barrier lets the workgroup sum the KW partials in
+//     wave order (deterministic) and run the epilogue on those tiles' outputs;
+//     the next tiles' loads are in flight meanwhile. So a workgroup may walk any
+//     number of tiles, and the grid can match the CUs exactly (no partial last
+//     round of workgroups).
 #include "ftk_device.h"
 #include "ftk_internal.h"
 
@@ -147,8 +150,59 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
     scale = 1.0f / sqrtf(total / (float)K + a.eps);
   }
 
-  // ---- tiles: stage each unit through LDS into the MFMAs, refill the window ------
-  int count = 0;
+  // ---- epilogue of parked tiles: thread e takes (tile i, subtile t, lane position ln)
+  // D[4 gg + r][ll] of subtile t: weight row 16 t + 4 gg + r of the tile, x row ll.
+  // part[0 .. n) holds the walk's tiles done .. done + n - 1 (tile wg + i grid).
+  constexpr int TO = (EPI == EPI_SWIGLU) ? T / 2 : T;  // output subtiles
+  const int outputs = gemv_outputs(EPI, a.N);
+  unsigned long long best = 0ull;
+  auto flush = [&](int n, int done) {
+    const int entries = n * TO * 64;
+    for (int e = tid; e < entries; e += 64 * KW) {
+      const int ln = e & 63, t = (e >> 6) % TO, i = e / (64 * TO);
+      const int ll = ln & 15, gg = ln >> 4;
+      if (ll >= M) continue;
+      const int tl = wg + (done + i) * (int)gridDim.x;
+      f32x4_t s = part[i][0][t][ln];
+#pragma unroll
+      for (int w = 1; w < KW; ++w) s += part[i][w][t][ln];
+      if constexpr (EPI == EPI_SWIGLU) {
+        f32x4_t u = part[i][0][t + T / 2][ln];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) u += part[i][w][t + T / 2][ln];
+        const int c0 = tl * 8 * T + t * 16 + 4 * gg;
+        uint16_t* yr = a.y + (size_t)ll * outputs;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (c0 + r < outputs) yr[c0 + r] = (uint16_t)swiglu_bf16(s[r], u[r]);
+      } else {
+        const int n0 = tl * 16 * T + t * 16 + 4 * gg;
+        uint32_t bits[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(s[r]);
+        if (a.y != nullptr) {
+          uint16_t* yr = a.y + (size_t)ll * a.N;
+          if (n0 + 3 < a.N && (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {
+            *reinterpret_cast<u32x2_t*>(yr + n0) = u32x2_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n0 + r < a.N) yr[n0 + r] = (uint16_t)bits[r];
+          }
+        }
+        if constexpr (EPI == EPI_ARGMAX) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n0 + r < a.N) best = key_max(best, argmax_key(bf16_to_f32(bits[r]), (uint32_t)(n0 + r)));
+        }
+      }
+    }
+  };
+
+  // ---- tiles: stage each unit through LDS into the MFMAs, refill the window.
+  // Every DMAX tiles (and after the last) the parked partials are summed and
+  // stored; the next tiles' loads stay in flight across those two barriers. ----
+  int count = 0, done = 0;
   for (;;) {
     const int next = tile + (int)gridDim.x;
     const bool more = next < tiles;
@@ -161,7 +215,7 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
     for (int j = 0; j < C; ++j) {
       const int q = j % U;
       if constexpr (PRO) {
-        if (count == 0) {  // first tile: normalise this segment of the slice in place
+        if (count == 0 && done == 0) {  // first tile: normalise this segment of the slice in place
 #pragma unroll
           for (int s = 0; s < 4; ++s) xr[j][s] = norm8(xr[j][s], gain[xoff(j, s) >> 3], scale);
         }
@@ -202,59 +256,19 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
 #pragma unroll
     for (int t = 0; t < T; ++t) part[count][kw][t][lane] = acc[t];
     ++count;
-    if (!more) break;
+    if (count == DMAX || !more) {  // workgroup-uniform: every wave walks the same tiles
+      __syncthreads();
+      flush(count, done);
+      done += count;
+      count = 0;
+      if (!more) break;
+      __syncthreads();  // the next tiles park in the same slots
+    }
     tile = next;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) wp[t][r] = wn[t][r];
-  }
-  __syncthreads();
-
-  // ---- epilogue: thread e takes (tile i, subtile t, lane position ln) ------------
-  // D[4 gg + r][ll] of subtile t: weight row 16 t + 4 gg + r of the tile, x row ll.
-  constexpr int TO = (EPI == EPI_SWIGLU) ? T / 2 : T;  // output subtiles
-  const int outputs = gemv_outputs(EPI, a.N);
-  unsigned long long best = 0ull;
-  const int entries = count * TO * 64;
-  for (int e = tid; e < entries; e += 64 * KW) {
-    const int ln = e & 63, t = (e >> 6) % TO, i = e / (64 * TO);
-    const int ll = ln & 15, gg = ln >> 4;
-    if (ll >= M) continue;
-    const int tl = wg + i * (int)gridDim.x;
-    f32x4_t s = part[i][0][t][ln];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) s += part[i][w][t][ln];
-    if constexpr (EPI == EPI_SWIGLU) {
-      f32x4_t u = part[i][0][t + T / 2][ln];
-#pragma unroll
-      for (int w = 1; w < KW; ++w) u += part[i][w][t + T / 2][ln];
-      const int c0 = tl * 8 * T + t * 16 + 4 * gg;
-      uint16_t* yr = a.y + (size_t)ll * outputs;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (c0 + r < outputs) yr[c0 + r] = (uint16_t)swiglu_bf16(s[r], u[r]);
-    } else {
-      const int n0 = tl * 16 * T + t * 16 + 4 * gg;
-      uint32_t bits[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(s[r]);
-      if (a.y != nullptr) {
-        uint16_t* yr = a.y + (size_t)ll * a.N;
-        if (n0 + 3 < a.N && (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {
-          *reinterpret_cast<u32x2_t*>(yr + n0) = u32x2_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n0 + r < a.N) yr[n0 + r] = (uint16_t)bits[r];
-        }
-      }
-      if constexpr (EPI == EPI_ARGMAX) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n0 + r < a.N) best = key_max(best, argmax_key(bf16_to_f32(bits[r]), (uint32_t)(n0 + r)));
-      }
-    }
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
@@ -327,9 +341,7 @@ hipError_t launch_stage(const ProjArgs& a, int epi, const StageShape& sh, hipStr
   const int c = quad_segments(a.K, sh.kw);
   StageKernel k = c > 0 ? pick_stage(sh.subtiles, c, sh.kw, sh.unroll, a.gamma != nullptr, epi) : nullptr;
   if (k == nullptr || a.M < 1 || a.M > kStageMaxRows) return hipErrorInvalidValue;
-  if (sh.grid < 1 || sh.grid > sh.tiles ||
-      (sh.tiles + sh.grid - 1) / sh.grid > stage_max_depth(sh.subtiles, sh.kw))
-    return hipErrorInvalidValue;
+  if (sh.grid < 1 || sh.grid > sh.tiles) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(sh.grid), dim3(64 * sh.kw), 0, stream, a, sh.tiles);
   return hipGetLastError();
 }

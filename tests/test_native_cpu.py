@@ -246,8 +246,9 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
                 assert p.threads == 64 * p.waves and k % (32 * p.waves) == 0
             if p.kind == _native.KIND_STAGE:
-                t = p.rows_per_wave // 16
-                assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 64 // (t * p.waves)
+                # any walk depth (the epilogue runs every 64 // (T KW) tiles); groups_per_cu workgroups per CU
+                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else 1
+                assert 1 <= p.grid <= min(p.tiles, 256 * gpc)
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_QUAD:
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
