@@ -83,6 +83,12 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
   // With the prologue, row li is x[li] or the gathered x[x_ids[li]], plus the residual.
   const uint16_t* xrow = (PRO && mine) ? x_row(a, li) : a.x + (size_t)(mine ? li : 0) * K;
   auto x_frag = [&](int j, int s) { return mine ? load16(xrow + xoff(j, s)) : u32x4_t{0u, 0u, 0u, 0u}; };
+  // x streamed beside the weights: lanes past the last row read row M - 1 again
+  // (in bounds). Unconditional loads keep branches out of the main loop (their
+  // joins would wait for each load); those lanes feed only MFMA output columns
+  // li >= M, which are never stored.
+  const uint16_t* xs_row = a.x + (size_t)(mine ? li : M - 1) * K;
+  auto x_stream = [&](int j, int s) { return load16(xs_row + xoff(j, s)); };
   u32x4_t xr[XS ? 1 : C][4];
   u32x4_t xv[XS ? U : 1][4];
   if constexpr (!XS) {
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
       for (int r = 0; r < 4; ++r) wv[q][t][r] = load_stream16(wp[t][r] + q * kStep);
     if constexpr (XS) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xv[q][s] = x_frag(q, s);
+      for (int s = 0; s < 4; ++s) xv[q][s] = x_stream(q, s);
     }
   }
 
@@ -240,7 +246,7 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
           for (int r = 0; r < 4; ++r) wv[q][t][r] = load_stream16(wp[t][r] + (j + U) * kStep);
         if constexpr (XS) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) xv[q][s] = x_frag(j + U, s);
+          for (int s = 0; s < 4; ++s) xv[q][s] = x_stream(j + U, s);
         }
       } else if (more) {
 #pragma unroll
@@ -249,7 +255,7 @@ __global__ __launch_bounds__(64 * KW) void stage_kernel(ProjArgs a, int tiles) {
           for (int r = 0; r < 4; ++r) wv[q][t][r] = load_stream16(wn[t][r] + (j + U - C) * kStep);
         if constexpr (XS) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) xv[q][s] = x_frag(j + U - C, s);
+          for (int s = 0; s < 4; ++s) xv[q][s] = x_stream(j + U - C, s);
         }
       }
     }
