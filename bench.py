@@ -16,7 +16,8 @@ JSON line with the contract fields plus ``roofline`` (dominant kernel: the
 fused gate/up + SwiGLU GEMV), ``cpu_baseline`` (the reference's torch CPU path on
 a bounded sample of the same workload) and ``per_shape`` (µs, GB/s and fraction
 of the 8 TB/s HBM roofline for every BASELINE configuration, plus the split-KV
-decode attention at Qwen3-8B heads).
+decode attention at Qwen3-8B heads, a whole decode layer and a whole greedy decode
+step of a Qwen3-8B-shape transformers model through decode.py).
 """
 
 import argparse
@@ -322,6 +323,7 @@ def main():
         per_shape = shapes_table(model, step, dev)
         per_shape.update(attention_table(cfg, dev))
         per_shape.update(full_layer_table(model, dev))
+        per_shape.update(decode_model_table(cfg, dev))
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -519,6 +521,42 @@ def full_layer_table(model, dev):
     del caches, graph
     stage("full decode layer done")
     return {f"C3 8B full decode layer M=1 (attention over {c} slots)": shape_entry(us, byts)}
+
+
+def decode_model_table(cfg, dev, context=FULL_LAYER_CONTEXT):
+    """One whole greedy decode step of a Qwen3-8B-shape transformers model (random weights) through
+    fast-transformer_amd/decode.py at B = 1, attending over ``context`` cached slots: embedding
+    gather + 36 layers + final norm + lm_head + argmax, one graph (engine/decode.py:215-297)."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    import decode as D
+
+    hf = Qwen3Config(vocab_size=cfg["vocab"], hidden_size=cfg["hidden"], intermediate_size=cfg["inter"],
+                     num_hidden_layers=cfg["layers"], num_attention_heads=cfg["q_heads"],
+                     num_key_value_heads=cfg["kv_heads"], head_dim=cfg["head_dim"], rms_norm_eps=EPS,
+                     rope_theta=1_000_000.0, tie_word_embeddings=False, max_position_embeddings=context)
+    default = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev), torch.no_grad():
+            hf_model = Qwen3ForCausalLM(hf).eval()
+    finally:
+        torch.set_default_dtype(default)
+    dec = D.Decoder(hf_model, 1, context)
+    g = torch.Generator(device=dev).manual_seed(17)
+    dec.cache.store.copy_(torch.randn(dec.cache.store.shape, generator=g, device=dev).to(torch.bfloat16))
+    dec.position.fill_(context - 1)
+    dec.token_ids.fill_(1234)
+    with torch.no_grad():
+        graph = capture(dec.step)
+    us = time_graph(graph, reps=10)
+    lb = layer_bytes(cfg, 1)
+    kv = 2 * cfg["layers"] * cfg["kv_heads"] * context * cfg["head_dim"] * 2
+    byts = cfg["layers"] * sum(lb.values()) + head_bytes(cfg, 1) + kv + 2 * cfg["hidden"]
+    del dec, hf_model, graph
+    stage("whole decode step done")
+    return {f"Qwen3-8B greedy decode step B=1 (transformers model through decode.py, attention over {context} "
+            f"slots)": {**shape_entry(us, byts), "tokens_per_s": round(1e6 / us, 1)}}
 
 
 def attention_table(cfg, dev):
