@@ -103,11 +103,42 @@ def test_grid_and_window_do_not_change_bits(cuda, gpc):
     x, w, g = _inputs(13, 12000, 4096, seed=3400, device=cuda)
     base = L.rms_norm_linear(x, g, 1e-6, w, config=cfg(1, 8, 2, 8))
     p = L.plan(13, 12000, 4096, config=cfg(1, 8, 2, gpc), prologue=True)
-    assert 1 <= -(-p.tiles // p.grid) <= 8
+    assert 1 <= p.grid <= p.tiles
     assert torch.equal(L.rms_norm_linear(x, g, 1e-6, w, config=cfg(1, 8, 2, gpc)), base)
     assert torch.equal(L.rms_norm_linear(x, g, 1e-6, w, config=cfg(1, 8, 4, gpc)), base)
     x2, w2, _ = _inputs(16, 3000, 12288, seed=3410, device=cuda)  # x streamed
     assert torch.equal(L.project(x2, w2, cfg(1, 8, 3, gpc)), L.project(x2, w2, cfg(1, 8, 4, 8)))
+
+
+@pytest.mark.parametrize("epi", ["store", "swiglu", "argmax"])
+def test_walks_longer_than_the_lds_depth(cuda, epi):
+    """One workgroup per CU walks more tiles than its LDS parks (8 with one subtile, 4 with two): the
+    epilogue runs every depth tiles inside the walk. The bits equal those of a grid whose walks fit,
+    and the oracle's bar holds."""
+    m, n, k = 5, 41000, 4096
+    t = 2 if epi == "swiglu" else 1
+    x, w, g = _inputs(m, n, k, seed=3600 + t, device=cuda)
+    epilogue = {"store": _native.EPI_STORE, "swiglu": _native.EPI_SWIGLU, "argmax": _native.EPI_ARGMAX}[epi]
+    long_walks, short_walks = cfg(t, 8, 2, 1), cfg(t, 8, 2, 16)
+    p = L.plan(m, n, k, epilogue, config=long_walks, prologue=True)
+    assert p.kind == _native.KIND_STAGE and -(-p.tiles // p.grid) > 64 // (8 * t)
+    q = L.plan(m, n, k, epilogue, config=short_walks, prologue=True)
+    assert -(-q.tiles // q.grid) <= 64 // (8 * t)
+    xb, wb, gb = to_bits(x), to_bits(w), to_bits(g)
+    if epi == "store":
+        got = L.rms_norm_linear(x, g, 1e-6, w, config=long_walks)
+        assert torch.equal(got, L.rms_norm_linear(x, g, 1e-6, w, config=short_walks))
+        assert within(to_bits(got), path.norm_project(xb, gb, 1e-6, wb))
+    elif epi == "swiglu":
+        got = S.gate_up_swiglu(x, w, g, 1e-6, config=long_walks)
+        assert torch.equal(got, S.gate_up_swiglu(x, w, g, 1e-6, config=short_walks))
+        assert within(to_bits(got), path.gate_up_swiglu(xb, wb, gb, 1e-6))
+    else:
+        ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=long_walks)
+        ids2, logits2 = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=short_walks)
+        assert torch.equal(ids, ids2) and torch.equal(logits, logits2)
+        assert within(to_bits(logits), path.lm_head_argmax(xb, wb, gb, 1e-6)[0])
+        np.testing.assert_array_equal(ids.cpu().numpy(), path.argmax_first(to_bits(logits)))
 
 
 @pytest.mark.parametrize("with_norm", [False, True])
