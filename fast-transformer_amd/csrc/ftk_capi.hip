@@ -795,7 +795,7 @@ int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride,
   if ((mode & FTK_ROPE_PREFILL) && (mode & FTK_ROPE_ROWS)) return FTK_ERR_INVALID;
   if ((mode & FTK_ROPE_TABLE) && (!(mode & FTK_ROPE_ROWS) || !phases)) return FTK_ERR_INVALID;
   if (!(mode & FTK_ROPE_PREFILL) && !position) return FTK_ERR_INVALID;
-  if (tokens > capacity || splits > 1 && split_stride < batch * tokens * (q_heads + 2 * kv_heads) * dim)
+  if (tokens > capacity || (splits > 1 && split_stride < batch * tokens * (q_heads + 2 * kv_heads) * dim))
     return FTK_ERR_INVALID;
   if (!(mode & FTK_ROPE_TABLE) && table_rows < ((mode & FTK_ROPE_ROWS) ? batch * tokens : tokens))
     return FTK_ERR_INVALID;  // shared [1, T, D] or per-row [B, T, D] rows must cover every phase
