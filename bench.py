@@ -128,6 +128,17 @@ class Step:
             hidden = L.linear(act, lw["down"])
         return hidden, resid
 
+    def layers_residual_epilogue(self):
+        """The same data flow with the residual add in the O and down epilogues (decode.py's form):
+        each norm then reads the stored stream as a plain x."""
+        resid = self.resid
+        for lw in self.model.layers:
+            L.rms_norm_linear(resid, lw["ln1"], EPS, lw["qkv"])
+            resid = L.linear_residual(self.attn, lw["o"], resid)
+            act = S.gate_up_swiglu(resid, lw["gate_up"], lw["ln2"], EPS)
+            resid = L.linear_residual(act, lw["down"], resid)
+        return resid
+
     def run(self):
         h = self.layers()
         return A.lm_head_argmax(h, self.model.head, self.model.final_norm, EPS, logits=True, top=self.top)
@@ -430,6 +441,10 @@ def shapes_table(model8, step8, dev):
     g = capture(step8.layers_residual)
     us = time_graph(g, reps=5) / cfg["layers"]
     out["C3 8B layer M=1, residual-add prologues"] = shape_entry(us, sum(lb.values()) + 4 * 2 * cfg["hidden"])
+    g = capture(step8.layers_residual_epilogue)
+    us = time_graph(g, reps=5) / cfg["layers"]
+    out["C3 8B layer M=1, residual add in the O / down epilogues"] = shape_entry(
+        us, sum(lb.values()) + 4 * 2 * cfg["hidden"])
     # C1 / C2: Qwen3-0.6B shapes
     model06 = Model(QWEN3_06B, dev, head=False, seed=2)
     st06 = Step(model06, 1, dev, seed=3)
@@ -486,8 +501,9 @@ FULL_LAYER_CONTEXT = 4096
 
 def full_layer_table(model, dev):
     """One whole M=1 decode layer on this library, per layer of the 36, at a 4K-slot cache:
-    residual-add norm + QKV, QK norm + RoPE + cache write, decode attention, O, residual-add
-    norm + gate/up + SwiGLU, down (engine/decode.py:229-261, engine/layers.py:32-90)."""
+    norm + QKV, QK norm + RoPE + cache write, decode attention, O with the residual add in its
+    epilogue, norm + gate/up + SwiGLU, down with the residual add in its epilogue
+    (engine/decode.py:229-261, engine/layers.py:32-90; decode.py's data flow)."""
     cfg = model.cfg
     hq, hkv, d, c = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"], FULL_LAYER_CONTEXT
     g = torch.Generator(device=dev).manual_seed(13)
@@ -500,19 +516,18 @@ def full_layer_table(model, dev):
     cos = torch.cat([angle, angle]).cos().to(torch.bfloat16).reshape(1, 1, d)
     sin = torch.cat([angle, angle]).sin().to(torch.bfloat16).reshape(1, 1, d)
     pos = torch.tensor([c - 1], device=dev, dtype=torch.int64)
-    hidden = torch.randn((1, cfg["hidden"]), generator=g, device=dev).to(torch.bfloat16)
     resid = torch.randn((1, cfg["hidden"]), generator=g, device=dev).to(torch.bfloat16)
 
     def layers():
-        h, r = hidden, resid
+        r = resid
         for lw, (k, v), (qn, kn) in zip(model.layers, caches, norms):
-            qkv, r = L.add_rms_norm_linear(h, r, lw["ln1"], EPS, lw["qkv"])
+            qkv = L.rms_norm_linear(r, lw["ln1"], EPS, lw["qkv"])
             q = R.qk_rope_cache(qkv.view(1, 1, -1), qn, kn, cos, sin, pos, k, v, hq)
             attn = DA.decode_attention(q, k, v, pos, d ** -0.5)
-            o = L.linear(attn.reshape(1, hq * d), lw["o"])
-            act, r = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS, residual=r)
-            h = L.linear(act, lw["down"])
-        return h, r
+            r = L.linear_residual(attn.reshape(1, hq * d), lw["o"], r)
+            act = S.gate_up_swiglu(r, lw["gate_up"], lw["ln2"], EPS)
+            r = L.linear_residual(act, lw["down"], r)
+        return r
 
     graph = capture(layers)
     us = time_graph(graph, reps=5) / len(model.layers)

@@ -551,9 +551,12 @@ static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_by
   return pa < pb + (uintptr_t)b_bytes && pb < pa + (uintptr_t)a_bytes;
 }
 
-int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma, float eps, const void* w, void* y,
-                          int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
-                          void* workspace, int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
+// Every projection entry point lands here; `out_add` (STORE only) is the residual
+// stream the rounded outputs are added to, or null.
+static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, float eps, const void* w, void* y,
+                        int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
+                        void* workspace, int64_t workspace_bytes, const ftk_config* cfg, const void* out_add,
+                        void* stream) {
   if (x == nullptr || w == nullptr) return FTK_ERR_INVALID;
   if (epilogue != FTK_EPI_ARGMAX && y == nullptr) return FTK_ERR_INVALID;
   if (epilogue == FTK_EPI_ARGMAX) {
@@ -585,7 +588,8 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (p.kind == FTK_KIND_GENERIC) {
     if (gamma != nullptr) return FTK_ERR_UNSUPPORTED;
-    return hip_status(launch_gemm_generic((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, (int)M, (int)N,
+    return hip_status(launch_gemm_generic((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y,
+                                          (const uint16_t*)out_add, (int)M, (int)N,
                                           (int)K, s));
   }
   if (!aligned16(x) || !aligned16(w) || (gamma && !aligned16(gamma))) return FTK_ERR_UNSUPPORTED;
@@ -606,6 +610,7 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
   a.sum = (uint16_t*)r.sum;
   a.x_ids = r.x_ids;
   a.x_ids_bytes = r.x_ids_bytes;
+  a.out_add = (const uint16_t*)out_add;
   // The MFMA kind's projection reads the pre-pass's stored rows: it needs sum.
   if (p.kind == FTK_KIND_MFMA && (r.residual != nullptr || r.x_ids != nullptr) && r.sum == nullptr)
     return FTK_ERR_UNSUPPORTED;
@@ -638,11 +643,36 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
   return hip_status(e);
 }
 
+int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma, float eps, const void* w, void* y,
+                          int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
+                          void* workspace, int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
+  return project_impl(x, rows, gamma, eps, w, y, M, N, K, epilogue, ids, ids_bytes, top, workspace, workspace_bytes,
+                      cfg, nullptr, stream);
+}
+
 int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w, void* y, int64_t M, int64_t N,
                      int64_t K, int epilogue, void* ids, int ids_bytes, float* top, void* workspace,
                      int64_t workspace_bytes, const ftk_config* cfg, void* stream) {
-  return ftk_project_rows_bf16(x, nullptr, gamma, eps, w, y, M, N, K, epilogue, ids, ids_bytes, top, workspace,
-                               workspace_bytes, cfg, stream);
+  return project_impl(x, nullptr, gamma, eps, w, y, M, N, K, epilogue, ids, ids_bytes, top, workspace,
+                      workspace_bytes, cfg, nullptr, stream);
+}
+
+int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
+                         int64_t K, const ftk_config* cfg, void* stream) {
+  if (residual == nullptr || y == nullptr) return FTK_ERR_INVALID;
+  // y may be the residual itself (each output reads its own residual element,
+  // then writes it), but no other overlap with the inputs.
+  const int64_t out_bytes = M * N * 2;
+  if (y != residual && overlaps(y, out_bytes, residual, out_bytes)) return FTK_ERR_INVALID;
+  if (overlaps(y, out_bytes, x, M * K * 2) || overlaps(y, out_bytes, w, N * K * 2)) return FTK_ERR_INVALID;
+  int st = project_impl(x, nullptr, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, cfg,
+                        residual, stream);
+  if (st == FTK_ERR_UNSUPPORTED && cfg == nullptr) {  // an unaligned pointer or an unsplit MFMA x slice
+    const ftk_config c = {FTK_KIND_GENERIC, 0, 0, 0, 0};
+    st = project_impl(x, nullptr, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, &c,
+                      residual, stream);
+  }
+  return st;
 }
 
 int ftk_linear_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {

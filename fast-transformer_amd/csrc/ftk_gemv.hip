@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         if constexpr (EPI == EPI_STORE) {
-          if (lane == 0) a.y[(size_t)m * a.N + col] = (uint16_t)f32_to_bf16(tot[p][m]);
+          if (lane == 0) a.y[(size_t)m * a.N + col] = (uint16_t)store_bits(a, tot[p][m], m, col);
         } else if constexpr (EPI == EPI_SWIGLU) {
           if (lane == 0) a.y[(size_t)m * (a.N / 2) + col] = (uint16_t)swiglu_bf16(tot[p][m], tot[PW + p][m]);
         } else {
@@ -249,7 +249,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(ProjArgs a, int tiles) {
 template <int MAXM>
 __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ w,
-                                                                uint16_t* __restrict__ y, int M, int N, int K) {
+                                                                uint16_t* y, const uint16_t* add, int M, int N,
+                                                                int K) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= N) return;  // whole wave leaves together; no barrier below
@@ -267,7 +268,11 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const uint16_t* 
   for (int m = 0; m < MAXM; ++m) {
     if (m < M) {
       const float s = wave_sum(acc[m]);
-      if (lane == 0) y[(size_t)m * N + row] = (uint16_t)f32_to_bf16(s);
+      if (lane == 0) {
+        const uint32_t b = f32_to_bf16(s);
+        y[(size_t)m * N + row] =
+            (uint16_t)(add == nullptr ? b : f32_to_bf16(bf16_to_f32(b) + bf16_to_f32(add[(size_t)m * N + row])));
+      }
     }
   }
 }
@@ -358,15 +363,15 @@ hipError_t launch_gemv(const ProjArgs& a, int epi, const GemvShape& s, hipStream
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
-                               hipStream_t stream) {
+hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, const uint16_t* add, int M, int N,
+                               int K, hipStream_t stream) {
   const int grid = (N + kWaves - 1) / kWaves;
   if (M <= 4)
-    hipLaunchKernelGGL(gemm_generic_kernel<4>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+    hipLaunchKernelGGL(gemm_generic_kernel<4>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, add, M, N, K);
   else if (M <= 16)
-    hipLaunchKernelGGL(gemm_generic_kernel<16>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+    hipLaunchKernelGGL(gemm_generic_kernel<16>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, add, M, N, K);
   else
-    hipLaunchKernelGGL(gemm_generic_kernel<32>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, M, N, K);
+    hipLaunchKernelGGL(gemm_generic_kernel<32>, dim3(grid), dim3(kThreads), 0, stream, x, w, y, add, M, N, K);
   return hipGetLastError();
 }
 

@@ -30,7 +30,18 @@ struct ProjArgs {
   uint16_t* sum;             // [M, K] or null
   const void* x_ids;         // [M] int32 / int64 row indices into x, or null
   int x_ids_bytes;
+  // EPI_STORE only: the residual stream the outputs are added to, or null. The
+  // stored value is then bf16(bf16(y) + out_add[m, n]) (the add of add_rms_norm
+  // moved into the producer; it may alias y).
+  const uint16_t* out_add;   // [M, N] or null
 };
+
+// The BF16 bits a STORE epilogue writes for output (m, n) with FP32 sum s.
+__device__ __forceinline__ uint32_t store_bits(const ProjArgs& a, float s, int m, int n) {
+  const uint32_t b = f32_to_bf16(s);
+  if (a.out_add == nullptr) return b;
+  return f32_to_bf16(bf16_to_f32(b) + bf16_to_f32(a.out_add[(size_t)m * a.N + n]));
+}
 
 // Row m of the prologue's x: x[x_ids[m]] (embedding gather) or x[m].
 __device__ __forceinline__ const uint16_t* x_row(const ProjArgs& a, int m) {
@@ -181,8 +192,8 @@ hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int
                                   float* top, hipStream_t stream);
 
 // Ragged or unaligned shapes: one wave per weight row, scalar loads, no prologue/epilogue.
-hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
-                               hipStream_t stream);
+hipError_t launch_gemm_generic(const uint16_t* x, const uint16_t* w, uint16_t* y, const uint16_t* add, int M, int N,
+                               int K, hipStream_t stream);
 
 // Standalone operators (the reference's separate kernels).
 hipError_t launch_rms_norm(const uint16_t* x, int64_t row_stride, const uint16_t* gamma, uint16_t* y, int rows,

@@ -145,13 +145,14 @@ __global__ __launch_bounds__(64 * W) void mfma_kernel(ProjArgs a, MfmaArgs p) {
       for (int mb = 0; mb < MB; ++mb) {
         if (!mok[mb]) continue;
         uint16_t* yr = a.y + (size_t)(li + 16 * mb) * a.N;
-        if (n0 + 3 < a.N && (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {
+        if (a.out_add == nullptr && n0 + 3 < a.N && (a.N & 3) == 0 &&
+            (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {
           *reinterpret_cast<u32x2_t*>(yr + n0) =
               u32x2_t{pack_bf16(acc[t][mb][0], acc[t][mb][1]), pack_bf16(acc[t][mb][2], acc[t][mb][3])};
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (n0 + r < a.N) yr[n0 + r] = (uint16_t)f32_to_bf16(acc[t][mb][r]);
+            if (n0 + r < a.N) yr[n0 + r] = (uint16_t)store_bits(a, acc[t][mb][r], li + 16 * mb, n0 + r);
         }
       }
     }

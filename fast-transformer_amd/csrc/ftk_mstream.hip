@@ -165,7 +165,12 @@ __global__ __launch_bounds__(64 * KW) void mstream_kernel(ProjArgs a, int tiles)
       const int n0 = tl * 16 * T + t * 16 + 4 * gg;
       uint32_t bits[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bits[r] = f32_to_bf16(s[r]);
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (EPI == EPI_STORE)
+          bits[r] = n0 + r < a.N ? store_bits(a, s[r], ll, n0 + r) : 0u;
+        else
+          bits[r] = f32_to_bf16(s[r]);
+      }
       if (a.y != nullptr) {
         uint16_t* yr = a.y + (size_t)ll * a.N;
         if (n0 + 3 < a.N && (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {

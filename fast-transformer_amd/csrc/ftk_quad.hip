@@ -228,7 +228,7 @@ __global__ __launch_bounds__(64 * W) void quad_kernel(ProjArgs a, int tiles) {
 #pragma unroll
       for (int k = 1; k < KW; ++k) s += part[i][g * KW + k][p][m];
       if constexpr (EPI == EPI_STORE) {
-        a.y[(size_t)m * a.N + col] = (uint16_t)f32_to_bf16(s);
+        a.y[(size_t)m * a.N + col] = (uint16_t)store_bits(a, s, m, col);
       } else if constexpr (EPI == EPI_SWIGLU) {
         float u = part[i][g * KW][PW + p][m];
 #pragma unroll

@@ -6,16 +6,20 @@ KVCache, forward_last for a decode token) and engine/layers.py:13-102
 One step, per row b at its device-side position p_b:
 
   layer 0   qkv, r = embed_rms_norm_linear(ids, E, ln1, W_qkv)   embedding gather + norm + QKV, one launch
-  layer l   qkv, r = add_rms_norm_linear(h, r, ln1, W_qkv)       residual add + norm + QKV, one launch
+  layer l   qkv    = rms_norm_linear(r, ln1, W_qkv)               norm + QKV, one launch
             q      = qk_rope_cache(qkv, ...)                      head norms + RoPE; K, V into slot p_b
             a      = decode attention over slots 0..p_b
-            o      = linear(a, W_o)
-            act, r = gate_up_swiglu(o, W_gu, ln2, residual=r)      residual add + norm + gate/up + SwiGLU
-            h      = linear(act, W_down)
-  final     ids, logits = lm_head_argmax(h, W_lm, norm, residual=r)   residual add + norm + lm_head + argmax
+            r      = linear_residual(a, W_o, r)                   O, the residual add in its epilogue
+            act    = gate_up_swiglu(r, W_gu, ln2)                 norm + gate/up + SwiGLU
+            r      = linear_residual(act, W_down, r)              down, the residual add in its epilogue
+  final     ids, logits = lm_head_argmax(r, W_lm, norm)           norm + lm_head + argmax
 
-That is 6 launches per layer (7 with a merge of attention splits) and one for
-the vocabulary. The weights are the model's own tensors (BF16, on the GPU),
+The reference adds each sublayer's output to the residual stream in the next
+norm (add_rms_norm, decode.py:236-243, :258-261, :291-296); here the add runs
+in the epilogue of the projection that produces it, which stores the same BF16
+sum, so no norm prologue has to read a second [rows, H] stream. That is 6
+launches per layer (7 with a merge of attention splits) and one for the
+vocabulary. The weights are the model's own tensors (BF16, on the GPU),
 packed once as the reference packs them ([Wq; Wk; Wv], [Wg; Wu],
 layers.py:23-26, :92-95). Positions, input ids and the RoPE phase live on the
 device, so one captured graph serves every step (``Decoder.capture``), the way
@@ -105,26 +109,24 @@ class Decoder:
     def step(self):
         """One decode token per row at ``position`` (engine/decode.py:215-297 for a one-token step)."""
         batch = self.batch
-        h = residual = None
+        residual = None
         for index, layer in enumerate(self.layers):
             eps = layer.input_norm.variance_epsilon
             if index == 0:
                 qkv, residual = _linear.embed_rms_norm_linear(self.token_ids, self.embed, layer.input_norm.weight,
                                                               eps, layer.qkv_weight)
             else:
-                qkv, residual = _linear.add_rms_norm_linear(h, residual, layer.input_norm.weight, eps,
-                                                            layer.qkv_weight)
+                qkv = _linear.rms_norm_linear(residual, layer.input_norm.weight, eps, layer.qkv_weight)
             keys, values = self.cache.keys[index], self.cache.values[index]
             query = _rope.qk_rope_cache(qkv.view(batch, 1, -1), layer.q_norm, layer.k_norm, self.cos, self.sin,
                                         self.position, keys, values, layer.q_heads, rows=True, phases=self.phases)
             attention = _attention.attend(query.reshape(batch, layer.q_heads, -1), keys, values, self.position,
                                           layer.scaling)
-            o = _linear.linear(attention.view(batch, -1), layer.o_weight)
-            act, residual = _swiglu.gate_up_swiglu(o, layer.gate_up_weight, layer.post_norm.weight,
-                                                   layer.post_norm.variance_epsilon, residual=residual)
-            h = _linear.linear(act, layer.down_weight)
-        return _argmax.lm_head_argmax(h, self.lm_head, self.norm.weight, self.norm.variance_epsilon,
-                                      residual=residual)
+            residual = _linear.linear_residual(attention.view(batch, -1), layer.o_weight, residual)
+            act = _swiglu.gate_up_swiglu(residual, layer.gate_up_weight, layer.post_norm.weight,
+                                         layer.post_norm.variance_epsilon)
+            residual = _linear.linear_residual(act, layer.down_weight, residual)
+        return _argmax.lm_head_argmax(residual, self.lm_head, self.norm.weight, self.norm.variance_epsilon)
 
     def advance(self, ids):
         """Feed ``ids`` as the next tokens and move every row one slot on (device-side, capturable)."""

@@ -83,6 +83,8 @@ SIGNATURES = {
                                        _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "ftk_project_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64, _int,
                                 _c_void_p, _int, _c_void_p, _c_void_p, _i64, ctypes.POINTER(Config), _c_void_p]),
+    "ftk_project_add_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                    ctypes.POINTER(Config), _c_void_p]),
     "ftk_project_rows_bf16": (_int, [_c_void_p, ctypes.POINTER(Rows), _c_void_p, _float, _c_void_p, _c_void_p,
                                      _i64, _i64, _i64, _int, _c_void_p, _int, _c_void_p, _c_void_p, _i64,
                                      ctypes.POINTER(Config), _c_void_p]),

@@ -266,6 +266,35 @@ def _choose(x, weight):
     return best
 
 
+def linear_residual(x, weight, residual, config=None):
+    """bf16(linear(x, weight) + residual): a projection whose output joins the residual stream.
+
+    The add of add_rms_norm (engine/kernels/rmsnorm.py:86-95) runs in the projection's epilogue
+    (ftk_project_add_bf16). Where engine/decode.py:236-243 / :258-261 add the O and down outputs to
+    the residual, the result is add_rms_norm's ``summed`` bit for bit, so the next norm reads it as a
+    plain x and no prologue reads the residual again. Neither input is modified. Every row count
+    runs this library's kernels (the MFMA kind from 17 rows).
+    """
+    _native.require_gpu(x, weight, residual)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
+        raise ValueError("linear_residual takes BF16 x, weight and residual")
+    if not weight.is_contiguous():
+        raise ValueError("linear_residual takes a contiguous [N, K] weight")
+    n, k = weight.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"x has K={x.shape[-1]}, weight has K={k}")
+    if tuple(residual.shape) != (*x.shape[:-1], n):
+        raise ValueError(f"residual must be {(*x.shape[:-1], n)}, got {tuple(residual.shape)}")
+    flat = _as_rows(x)
+    res = residual.reshape(-1, n).contiguous()
+    m = flat.shape[0]
+    out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    cfg = ctypes.byref(config) if config is not None else None
+    _native.call("ftk_project_add_bf16", _native.ptr(flat), _native.ptr(weight), _native.ptr(res), _native.ptr(out),
+                 m, n, k, cfg, _native.stream_of(flat))
+    return out.reshape(*x.shape[:-1], n)
+
+
 def keep_native(rows, weight):
     """Leave a shape on torch's native GEMM without tuning it (linear.py:484-486)."""
     _CHOICES.setdefault((weight.device, rows, weight.shape[0], weight.shape[1]), "native")

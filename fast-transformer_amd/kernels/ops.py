@@ -12,6 +12,7 @@ and take part in FakeTensor shape propagation. Mutated arguments are declared
 
 Registered:
   ftk::linear(x, weight)                                    engine/kernels/linear.py:489-523
+  ftk::linear_residual(x, weight, residual)                 linear + the add of rmsnorm.py:86-95 in its epilogue
   ftk::rms_norm_linear(x, norm_weight, eps, weight)         rmsnorm.py:49-72 + linear
   ftk::add_rms_norm_linear(x, residual, norm_weight, eps, weight) -> (y, summed)
   ftk::gate_up_swiglu(x, gate_up_weight, norm_weight?, eps) swiglu.py:13-40 fused into the projection
@@ -50,6 +51,16 @@ def linear(x: Tensor, weight: Tensor) -> Tensor:
 
 @linear.register_fake
 def _(x, weight):
+    return x.new_empty((*x.shape[:-1], weight.shape[0]))
+
+
+@torch.library.custom_op("ftk::linear_residual", mutates_args=())
+def linear_residual(x: Tensor, weight: Tensor, residual: Tensor) -> Tensor:
+    return _linear.linear_residual(x, weight, residual)
+
+
+@linear_residual.register_fake
+def _(x, weight, residual):
     return x.new_empty((*x.shape[:-1], weight.shape[0]))
 
 

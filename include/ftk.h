@@ -176,6 +176,19 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
                           int64_t M, int64_t N, int64_t K, int epilogue, void* ids, int ids_bytes, float* top,
                           void* workspace, int64_t workspace_bytes, const ftk_config* cfg, void* stream);
 
+/* y = bf16( f32(bf16(x @ w^T)) + f32(residual) ), [M, N]: the projection whose
+ * output joins the residual stream, with the add of add_rms_norm
+ * (engine/kernels/rmsnorm.py:86-95) moved into its epilogue. At the reference's
+ * call sites (engine/decode.py:236-243 and :258-261, the O and down projections
+ * of engine/layers.py:86 and :101-102 followed by add_rms_norm) the stored value
+ * is exactly add_rms_norm's `summed` output, so the next norm can read it as a
+ * plain x (ftk_rms_norm_linear_bf16 and friends) and no prologue reads the
+ * residual again. `y` may be `residual` itself (in place); no other overlap.
+ * No reference counterpart as one call: it fuses linear.py:489-523 with the add
+ * of rmsnorm.py:98-125. cfg may be NULL. */
+int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
+                         int64_t K, const ftk_config* cfg, void* stream);
+
 /* ---- standalone operators ---------------------------------------------------- */
 
 /* rms_norm(x, weight, eps) (engine/kernels/rmsnorm.py:49-72): x rows of

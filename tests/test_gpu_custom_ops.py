@@ -21,6 +21,8 @@ def test_ops_equal_the_functions(cuda):
     g = seeded((1024,), seed=3, scale=0.1, shift=1.0, device=cuda)
     r = seeded((3, 1024), seed=4, device=cuda)
     assert torch.equal(torch.ops.ftk.linear(x, w), L.linear(x, w))
+    r4 = seeded((3, 4096), seed=11, device=cuda)
+    assert torch.equal(torch.ops.ftk.linear_residual(x, w, r4), L.linear_residual(x, w, r4))
     assert torch.equal(torch.ops.ftk.rms_norm_linear(x, g, 1e-6, w), L.rms_norm_linear(x, g, 1e-6, w))
     for got, want in zip(torch.ops.ftk.add_rms_norm_linear(x, r, g, 1e-6, w), L.add_rms_norm_linear(x, r, g, 1e-6, w)):
         assert torch.equal(got, want)
@@ -39,7 +41,9 @@ def test_opcheck_schema_and_fake(cuda):
     x = seeded((2, 512), seed=8, device=cuda)
     w = seeded((256, 512), seed=9, scale=0.02, device=cuda)
     g = seeded((512,), seed=10, scale=0.1, shift=1.0, device=cuda)
+    r = seeded((2, 256), seed=12, device=cuda)
     for op, args in ((torch.ops.ftk.linear.default, (x, w)), (torch.ops.ftk.rms_norm_linear.default, (x, g, 1e-6, w)),
+                     (torch.ops.ftk.linear_residual.default, (x, w, r)),
                      (torch.ops.ftk.swiglu.default, (x,))):
         torch.library.opcheck(op, args, test_utils=("test_schema", "test_faketensor"))
 

@@ -61,6 +61,14 @@ def test_invalid_arguments_rejected_before_any_launch():
     assert lib.ftk_project_bf16(fake, None, 0.0, fake, None, 1, 64, 64, _native.EPI_ARGMAX, fake, 8, None, None, 0,
                                 None, None) in (_native.FTK_ERR_WORKSPACE, _native.FTK_ERR_HIP)
     assert lib.ftk_argmax_bf16(fake, 1, 8, fake, 3, None, fake, 64, None) == _native.FTK_ERR_INVALID
+    # the epilogue's residual add needs a residual, and y may overlap only the residual itself
+    x, w, r, y = (ctypes.c_void_p(a) for a in (1 << 16, 1 << 18, 1 << 20, 1 << 22))
+    assert lib.ftk_project_add_bf16(x, w, None, y, 1, 64, 64, None, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_project_add_bf16(x, w, r, None, 1, 64, 64, None, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_project_add_bf16(x, w, r, ctypes.c_void_p((1 << 20) + 2), 1, 64, 64, None, None) \
+        == _native.FTK_ERR_INVALID
+    assert lib.ftk_project_add_bf16(x, w, r, ctypes.c_void_p((1 << 16) + 64), 1, 64, 64, None, None) \
+        == _native.FTK_ERR_INVALID
     # the prologue's stored rows may not alias its inputs or outputs, and need the norm
     buf = ctypes.c_void_p(4096)
     rows = _native.Rows(buf, buf, None, 0)

@@ -6,7 +6,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 
 import kernels.ops  # noqa: F401  (registers torch.ops.ftk.*)
 
-NAMES = ("linear", "rms_norm_linear", "add_rms_norm_linear", "gate_up_swiglu", "lm_head_argmax", "rms_norm",
+NAMES = ("linear", "linear_residual", "rms_norm_linear", "add_rms_norm_linear", "gate_up_swiglu", "lm_head_argmax", "rms_norm",
          "add_rms_norm", "swiglu", "argmax", "decode_attention", "qk_rope_cache")
 
 
@@ -22,6 +22,7 @@ def test_fake_shapes():
         w = torch.empty(6144, 4096, dtype=bf)
         g = torch.empty(4096, dtype=bf)
         assert torch.ops.ftk.linear(x, w).shape == (5, 6144)
+        assert torch.ops.ftk.linear_residual(x, w, torch.empty(5, 6144, dtype=bf)).shape == (5, 6144)
         assert torch.ops.ftk.rms_norm_linear(x, g, 1e-6, w).shape == (5, 6144)
         y, s = torch.ops.ftk.add_rms_norm_linear(x, x, g, 1e-6, w)
         assert y.shape == (5, 6144) and s.shape == (5, 4096)
