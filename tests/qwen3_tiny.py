@@ -11,9 +11,11 @@ from transformers import Qwen3Config, Qwen3ForCausalLM
 
 from conftest import to_bits
 
-#: (hidden, intermediate, q_heads, kv_heads, head_dim): a small model, and Qwen3-0.6B's layer dimensions.
+#: (hidden, intermediate, q_heads, kv_heads, head_dim): a small model, and Qwen3-0.6B's and Qwen3-8B's
+#: layer dimensions.
 SMALL = (512, 1536, 8, 4, 128)
 QWEN3_06B = (1024, 3072, 16, 8, 128)
+QWEN3_8B = (4096, 12288, 32, 8, 128)
 
 
 def model(dims=SMALL, vocab=4096, layers=2, seed=0):

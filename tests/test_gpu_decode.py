@@ -3,10 +3,13 @@
 The decoder runs a prompt one token per step and then generates; the oracle's
 composed step (oracle/decode.py) is run teacher-forced on the same tokens.
 Bars: logits within |d| <= 2e-2 + 1e-2 |ref| of the oracle's and of
-transformers' float32 model on the same sequence; greedy ids equal to the
-oracle's wherever its top-2 gap exceeds 5e-2; caches within the same bar of
-the oracle's. A replayed graph of one step gives the eager results bit for bit.
+transformers' float32 model on the same sequence (wider at Qwen3-8B's width,
+where the logits are larger: see BARS); greedy ids equal to the oracle's
+wherever its top-2 gap exceeds 2.5x the bar's atol; caches within the same bar
+of the oracle's. A replayed graph of one step gives the eager results bit for bit.
 """
+
+import copy
 
 import numpy as np
 import pytest
@@ -23,12 +26,20 @@ pytestmark = pytest.mark.gpu
 
 def _setup(dims, batch, capacity, seed=5, length=6):
     m = Q.model(dims)
-    gpu = Q.model(dims).to("cuda", torch.bfloat16)
+    gpu = copy.deepcopy(m).to("cuda", torch.bfloat16)
     prompt = torch.randint(0, m.config.vocab_size, (batch, length), generator=torch.Generator().manual_seed(seed))
     return m, gpu, prompt
 
 
-@pytest.mark.parametrize("dims,batch", [(Q.SMALL, 1), (Q.SMALL, 2), (Q.QWEN3_06B, 1), (Q.QWEN3_06B, 4)])
+#: Bars (atol, rtol) against the oracle and against transformers' float32 model. At Qwen3-8B's
+#: width the logits are ~4x larger (std 1.3) and BF16 rounding alone (transformers run in BF16)
+#: moves them by up to 0.07 from float32, so that case takes a bar scaled to it.
+BARS = {Q.SMALL: ((2e-2, 1e-2), (2e-2, 1e-2)), Q.QWEN3_06B: ((2e-2, 1e-2), (2e-2, 1e-2)),
+        Q.QWEN3_8B: ((5e-2, 2e-2), (0.1, 2e-2))}
+
+
+@pytest.mark.parametrize("dims,batch", [(Q.SMALL, 1), (Q.SMALL, 2), (Q.QWEN3_06B, 1), (Q.QWEN3_06B, 4),
+                                        (Q.QWEN3_8B, 2)])
 def test_generate_matches_oracle_and_transformers(cuda, dims, batch):
     capacity, steps = 24, 5
     m, gpu, prompt = _setup(dims, batch, capacity)
@@ -40,19 +51,20 @@ def test_generate_matches_oracle_and_transformers(cuda, dims, batch):
     w, cfg = Q.weights(m, dec.cos.cpu(), dec.sin.cpu())
     o_ids, o_logits, o_keys, o_values = Q.oracle_run(decode, w, cfg, tokens, batch, capacity,
                                                      m.config.num_hidden_layers)
+    (oa, orl), (ta, trl) = BARS[dims]
     got = bf16.to_f32(to_bits(logits))
-    assert Q.close(got, o_logits)
-    ok, checked = Q.clear_ids_agree(ids.cpu().numpy(), o_logits[:, length - 1:], margin=5e-2)
+    assert Q.close(got, o_logits, oa, orl)
+    ok, checked = Q.clear_ids_agree(ids.cpu().numpy(), o_logits[:, length - 1:], margin=2.5 * oa)
     assert ok and checked >= batch * steps // 2
     with torch.no_grad():
         want = m(torch.from_numpy(tokens)).logits.numpy()
-    assert Q.close(got, want)
+    assert Q.close(got, want, ta, trl)
     n = tokens.shape[1]
     for layer in range(m.config.num_hidden_layers):
         k = bf16.to_f32(to_bits(dec.cache.keys[layer]))
         v = bf16.to_f32(to_bits(dec.cache.values[layer]))
-        assert Q.close(k[:, :, :n], bf16.to_f32(o_keys[layer][:, :, :n]))
-        assert Q.close(v[:, :, :n], bf16.to_f32(o_values[layer][:, :, :n]))
+        assert Q.close(k[:, :, :n], bf16.to_f32(o_keys[layer][:, :, :n]), oa, orl)
+        assert Q.close(v[:, :, :n], bf16.to_f32(o_values[layer][:, :, :n]), oa, orl)
         assert not k[:, :, n:].any() and not v[:, :, n:].any()
 
 
