@@ -275,7 +275,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU form in this build "
-              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(each GPU would run the same kernels on its shard of the weights); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
 
     dev = torch.device("cuda:0")
