@@ -502,9 +502,10 @@ FULL_LAYER_CONTEXT = 4096
 
 def full_layer_table(model, dev):
     """One whole M=1 decode layer on this library, per layer of the 36, at a 4K-slot cache:
-    norm + QKV, QK norm + RoPE + cache write, decode attention, O with the residual add in its
-    epilogue, norm + gate/up + SwiGLU, down with the residual add in its epilogue
-    (engine/decode.py:229-261, engine/layers.py:32-90; decode.py's data flow)."""
+    norm + QKV, QK norm + RoPE + cache write in the decode attention's prologue, O with the
+    residual add in its epilogue, norm + gate/up + SwiGLU, down with the residual add in its
+    epilogue (engine/decode.py:229-261, engine/layers.py:32-90; decode.py's data flow); and the
+    same layer with QK norm + RoPE + cache write as a launch of its own."""
     cfg = model.cfg
     hq, hkv, d, c = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"], FULL_LAYER_CONTEXT
     g = torch.Generator(device=dev).manual_seed(13)
@@ -513,30 +514,39 @@ def full_layer_table(model, dev):
     norms = [(_Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS),
               _Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS))
              for _ in model.layers]
-    angle = (c - 1) / 1_000_000.0 ** (torch.arange(0, d, 2, device=dev, dtype=torch.float64) / d)
-    cos = torch.cat([angle, angle]).cos().to(torch.bfloat16).reshape(1, 1, d)
-    sin = torch.cat([angle, angle]).sin().to(torch.bfloat16).reshape(1, 1, d)
+    angle = torch.arange(c, device=dev, dtype=torch.float64)[:, None] / \
+        1_000_000.0 ** (torch.arange(0, d, 2, device=dev, dtype=torch.float64) / d)
+    cos = torch.cat([angle, angle], dim=1).cos().to(torch.bfloat16)  # whole [C, D] tables, as decode.py's
+    sin = torch.cat([angle, angle], dim=1).sin().to(torch.bfloat16)
     pos = torch.tensor([c - 1], device=dev, dtype=torch.int64)
+    phases = torch.zeros((1, 1), device=dev, dtype=torch.int64)
     resid = torch.randn((1, cfg["hidden"]), generator=g, device=dev).to(torch.bfloat16)
 
-    def layers():
+    def layers(fused):
         r = resid
         for lw, (k, v), (qn, kn) in zip(model.layers, caches, norms):
             qkv = L.rms_norm_linear(r, lw["ln1"], EPS, lw["qkv"])
-            q = R.qk_rope_cache(qkv.view(1, 1, -1), qn, kn, cos, sin, pos, k, v, hq)
-            attn = DA.decode_attention(q, k, v, pos, d ** -0.5)
+            if fused:
+                attn = DA.rope_attend(qkv, qn, kn, cos, sin, pos, k, v, hq, d ** -0.5, phases=phases)
+            else:
+                q = R.qk_rope_cache(qkv.view(1, 1, -1), qn, kn, cos, sin, pos, k, v, hq, rows=True, phases=phases)
+                attn = DA.decode_attention(q, k, v, pos, d ** -0.5)
             r = L.linear_residual(attn.reshape(1, hq * d), lw["o"], r)
             act = S.gate_up_swiglu(r, lw["gate_up"], lw["ln2"], EPS)
             r = L.linear_residual(act, lw["down"], r)
         return r
 
-    graph = capture(layers)
-    us = time_graph(graph, reps=5) / len(model.layers)
     lb = layer_bytes(cfg, 1)
     byts = sum(lb.values()) + 4 * 2 * cfg["hidden"] + 2 * hkv * c * d * 2
-    del caches, graph
+    out = {}
+    for fused, name in ((True, ""), (False, ", QK norm + RoPE launched apart")):
+        graph = capture(lambda: layers(fused))
+        us = time_graph(graph, reps=5) / len(model.layers)
+        out[f"C3 8B full decode layer M=1 (attention over {c} slots{name})"] = shape_entry(us, byts)
+        del graph
+    del caches
     stage("full decode layer done")
-    return {f"C3 8B full decode layer M=1 (attention over {c} slots)": shape_entry(us, byts)}
+    return out
 
 
 def decode_model_table(cfg, dev, context=FULL_LAYER_CONTEXT):

@@ -246,7 +246,77 @@ __device__ __forceinline__ float head_max(float v) {
   return fmaxf(v, __shfl_xor(v, 32));
 }
 
-template <int G, int W, int NG>
+// Lane l ^ 32's value: v_permlane32_swap trades lanes 32..63 of its first
+// operand with lanes 0..31 of its second; with both = v, the second comes
+// back holding v[l + 32] in lanes 0..31 and the first v[l - 32] in lanes 32..63.
+__device__ __forceinline__ float lane_xor32(float v, int lane) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, lane < 32 ? p[1] : p[0]);
+}
+
+// Lane l ^ 16's value: v_permlane16_swap trades the odd 16-lane rows of its
+// first operand with the even rows of its second.
+__device__ __forceinline__ float lane_xor16(float v, int lane) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (lane & 16) ? p[0] : p[1]);
+}
+
+// Sum over the 16 lanes that share lane bits 0..1, the same bits in all of
+// them, on the VALU. row_ror:8 is lane ^ 8 inside a row of 16; its sum is the
+// same under ^ 8, so row_ror:4 (which reaches l ^ 4 or l ^ 12) adds lane ^ 4's
+// value. Every step adds a lane pair in both orders.
+__device__ __forceinline__ float quad_group_sum(float v, int lane) {
+  v += dpp<0x128, 0xF>(v);  // row_ror:8
+  v += dpp<0x124, 0xF>(v);  // row_ror:4
+  v += lane_xor16(v, lane);
+  return v + lane_xor32(v, lane);
+}
+
+// Head RMSNorm, gain and RoPE of one D = 128 head in the QUAD layout: lane
+// 4 c + i holds elements 8 c .. 8 c + 7 (c = 0..15), the 16 lanes of one i the
+// whole head; element j + 64 of element j's rotation is in chunk c ^ 8, lane ^ 32.
+// n = bf16(x / sqrt(mean(x^2) + eps)), w = bf16(n g),
+// out = bf16(bf16(w cos) + bf16(rotate_half(w) sin)) (engine/kernels/qk_rope.py:48-76).
+__device__ __forceinline__ u32x4_t quad_head_rope(u32x4_t x, u32x4_t g, u32x4_t c, u32x4_t s, float eps,
+                                                  int lane) {
+  float xf[8], gf[8], cf[8], sf[8];
+  widen8(x, xf);
+  widen8(g, gf);
+  widen8(c, cf);
+  widen8(s, sf);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+  ss = quad_group_sum(ss, lane);
+  const float inv_std = 1.0f / sqrtf(ss / 128.f + eps);
+  float w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = round_bf16(round_bf16(xf[e] * inv_std) * gf[e]);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = 2 * i + j;
+      const float partner = lane_xor32(w[e], lane);
+      const float rot = lane < 32 ? -partner : partner;  // chunk < 8: the first half of the head
+      r[j] = round_bf16(w[e] * cf[e]) + round_bf16(rot * sf[e]);
+    }
+    o[i] = pack_bf16(r[0], r[1]);
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// ROPE: the query heads are normalised and rotated here from the packed QKV
+// row, and the split whose interval holds the row's own slot (the position,
+// when it lies inside the cache) takes that slot's key and value from the
+// packed row too: it writes them to the cache, reads only the slots before
+// it from memory, and starts wave 0's softmax state with the new slot
+// (score s, p = 1). No other workgroup of the launch reads that slot.
+template <int G, int W, int NG, bool ROPE>
 __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
   constexpr int D = 128, SLOTS = 16 * NG;  // a unit: NG groups of 16 cache rows
   __shared__ float p_lds[W][64];
@@ -259,10 +329,37 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
   const int group = blockIdx.x / a.splits, split = blockIdx.x - group * a.splits;
   const int row = group / a.kv_heads;
   const int64_t newest = a.position[a.pos_stride * row];
+  int64_t shift = 0;  // RoPE phase - position
+  if constexpr (ROPE) {
+    // One load either way (the position again without phases), in flight beside the position's.
+    const int64_t loaded = *(a.phases != nullptr ? a.phases + row : a.position + a.pos_stride * row);
+    shift = a.phases != nullptr ? loaded : 0;
+  }
   const int64_t visible = newest + 1 < (int64_t)a.capacity ? newest + 1 : (int64_t)a.capacity;
   const int begin = split * a.chunk;
-  const int end = (int)(begin + a.chunk < visible ? begin + a.chunk : visible);
+  int end = (int)(begin + a.chunk < visible ? begin + a.chunk : visible);
+  bool own = ROPE && newest >= begin && newest < (int64_t)begin + a.chunk && newest < (int64_t)a.capacity;
+  if (own) end = (int)newest;
   const int units = end > begin ? (end - begin + SLOTS - 1) / SLOTS : 0;
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+
+  // ROPE: every load of the new token's heads goes out before the cache loads.
+  u32x4_t xq = zero, xk = zero, vnew = zero, gq = zero, gk = zero, cs = zero, sn = zero;
+  if constexpr (ROPE) {
+    const int kvh = group - row * a.kv_heads;
+    const uint16_t* src = a.packed + (size_t)row * (a.q_heads + 2 * a.kv_heads) * D + chunk * 8;
+    if (i4 < G) xq = load16(src + (size_t)(kvh * G + i4) * D);
+    xk = load16(src + (size_t)(a.q_heads + kvh) * D);
+    vnew = load16(src + (size_t)(a.q_heads + a.kv_heads + kvh) * D);
+    gq = load16(a.q_gain + chunk * 8);
+    gk = load16(a.k_gain + chunk * 8);
+    // A phase outside the tables reads row 0 instead and writes no slot (the row's output is unspecified).
+    const int64_t phase = newest + shift;
+    const int64_t at = phase >= 0 && phase < a.table_rows ? phase : 0;
+    if (at != phase) own = false;
+    cs = load16(a.cos + at * D + chunk * 8);
+    sn = load16(a.sin + at * D + chunk * 8);
+  }
 
   // K and V through buffer descriptors whose range ends at row `end`: a load
   // of a later row returns zeros without touching memory. So the ragged last
@@ -272,8 +369,10 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
   const uint32_t limit = end > 0 ? (uint32_t)end * (D * 2) : 0u;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k + cache), 0, limit, kBufferFlags);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v + cache), 0, limit, kBufferFlags);
-  const u32x4_t zero = {0u, 0u, 0u, 0u};
-  const u32x4_t qv = i4 < G ? load16(a.q + ((size_t)group * G + i4) * D + chunk * 8) : zero;
+  u32x4_t qv = zero;
+  if constexpr (!ROPE) {
+    if (i4 < G) qv = load16(a.q + ((size_t)group * G + i4) * D + chunk * 8);
+  }
   const int srow = 4 * ((lane >> 2) & 3) + ((lane >> 4) & 3);  // row of this lane's score in a group
 
   float m = -INFINITY, l = 0.f;  // head (lane & 3)'s softmax state, the same in its 16 lanes
@@ -297,6 +396,32 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
       kr[g][u] = buffer_load16(krs, at(wave, g, u));
       vr[g][u] = buffer_load16(vrs, at(wave, g, u));
     }
+  if constexpr (ROPE) {
+    // Keep the cache loads above: the head arithmetic waits for the head loads only.
+    __builtin_amdgcn_sched_barrier(0);
+    qv = quad_head_rope(xq, gq, cs, sn, a.q_eps, lane);
+    if (i4 >= G) qv = zero;
+    if (own) {
+      const u32x4_t knew = quad_head_rope(xk, gk, cs, sn, a.k_eps, lane);
+      if (wave == 0) {
+        if (i4 == 0) {
+          store16(a.k_store + cache + (size_t)newest * D + chunk * 8, knew);
+          store16(a.v_store + cache + (size_t)newest * D + chunk * 8, vnew);
+        }
+        // The new slot's score for head i4, in the head's 16 lanes; p = exp2(s - s) = 1.
+        m = quad_group_sum(dot8(knew, qv, 0.f), lane) * a.scale_log2;
+        l = 1.f;
+        if (i4 == 0) {
+          float vf[8];
+          widen8(vnew, vf);
+#pragma unroll
+          for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = vf[e];
+        }
+      }
+    }
+  }
   for (int unit = wave; unit < units; unit += W) {
     const int next = unit + W;
 #pragma unroll
@@ -531,22 +656,29 @@ static hipError_t launch_for_dim(const AttnArgs& a, const AttnShape& s, hipStrea
   }
 }
 
-template <int G>
+template <int G, bool ROPE>
 static hipError_t launch_quad_for_group(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
   const dim3 grid((unsigned)(s.groups * s.splits));
-  if (s.waves == 4 && s.unroll == 1) hipLaunchKernelGGL((attn_quad_kernel<G, 4, 1>), grid, dim3(256), 0, stream, a);
-  if (s.waves == 4 && s.unroll == 2) hipLaunchKernelGGL((attn_quad_kernel<G, 4, 2>), grid, dim3(256), 0, stream, a);
-  if (s.waves == 8 && s.unroll == 1) hipLaunchKernelGGL((attn_quad_kernel<G, 8, 1>), grid, dim3(512), 0, stream, a);
-  if (s.waves == 8 && s.unroll == 2) hipLaunchKernelGGL((attn_quad_kernel<G, 8, 2>), grid, dim3(512), 0, stream, a);
+  if (s.waves == 4 && s.unroll == 1)
+    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 1, ROPE>), grid, dim3(256), 0, stream, a);
+  else if (s.waves == 4 && s.unroll == 2)
+    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 2, ROPE>), grid, dim3(256), 0, stream, a);
+  else if (s.waves == 8 && s.unroll == 1)
+    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 1, ROPE>), grid, dim3(512), 0, stream, a);
+  else if (s.waves == 8 && s.unroll == 2)
+    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 2, ROPE>), grid, dim3(512), 0, stream, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
+template <bool ROPE>
 static hipError_t launch_quad(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
   switch (s.group_size) {
-    case 1: return launch_quad_for_group<1>(a, s, stream);
-    case 2: return launch_quad_for_group<2>(a, s, stream);
-    case 3: return launch_quad_for_group<3>(a, s, stream);
-    case 4: return launch_quad_for_group<4>(a, s, stream);
+    case 1: return launch_quad_for_group<1, ROPE>(a, s, stream);
+    case 2: return launch_quad_for_group<2, ROPE>(a, s, stream);
+    case 3: return launch_quad_for_group<3, ROPE>(a, s, stream);
+    case 4: return launch_quad_for_group<4, ROPE>(a, s, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -562,7 +694,10 @@ bool attn_supported(int kind, int dim, int group_size, int waves, int unroll) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
-  hipError_t e = s.kind == FTK_ATTN_QUAD ? launch_quad(a, s, stream)
+  // The head norm + RoPE prologue exists for the QUAD kind only (the caller checks).
+  if (a.packed != nullptr && s.kind != FTK_ATTN_QUAD) return hipErrorInvalidValue;
+  hipError_t e = s.kind == FTK_ATTN_QUAD ? (a.packed != nullptr ? launch_quad<true>(a, s, stream)
+                                                                 : launch_quad<false>(a, s, stream))
                  : s.dim == 128          ? launch_for_dim<128>(a, s, stream)
                                          : launch_for_dim<64>(a, s, stream);
   if (e != hipSuccess || s.splits == 1) return e;

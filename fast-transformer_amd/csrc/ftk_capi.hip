@@ -390,7 +390,11 @@ static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, i
   if ((D != 64 && D != 128) || G > kAttnMaxGroup) return FTK_ERR_UNSUPPORTED;
   if (C > INT32_MAX / 2 || B * Hkv > INT32_MAX / 2) return FTK_ERR_INVALID;
   const int groups = (int)(B * Hkv);
-  int kind = cfg && cfg->kind ? cfg->kind : (D == 128 && G <= 4 ? FTK_ATTN_QUAD : FTK_ATTN_ROWS);
+  // QUAD addresses a (row, KV head) cache with 32-bit byte offsets, reaching
+  // up to 9 x 32 slots past its end (the ragged last unit and the next step's loads).
+  const bool quad_fits = (C + 512) * D * 2 <= (int64_t)UINT32_MAX;
+  int kind = cfg && cfg->kind ? cfg->kind : (D == 128 && G <= 4 && quad_fits ? FTK_ATTN_QUAD : FTK_ATTN_ROWS);
+  if (kind == FTK_ATTN_QUAD && !quad_fits) return FTK_ERR_UNSUPPORTED;
   const int waves = cfg && cfg->waves ? cfg->waves : 4;
   int unroll = cfg && cfg->unroll ? cfg->unroll : (kind == FTK_ATTN_QUAD ? 1 : 4);
   if (kind == FTK_ATTN_ROWS && !(cfg && cfg->unroll) && !attn_supported(kind, (int)D, (int)G, waves, unroll))
@@ -776,19 +780,23 @@ int64_t ftk_decode_attention_workspace_bytes(int64_t batch, int64_t q_heads, int
   return p.workspace_bytes;
 }
 
-int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const int64_t* position,
-                              int positions, void* out, int64_t batch, int64_t q_heads, int64_t kv_heads,
-                              int64_t capacity, int64_t dim, double scale, void* workspace, int64_t workspace_bytes,
-                              const ftk_attn_config* cfg, void* stream) {
-  if (!q || !k || !v || !position || !out) return FTK_ERR_INVALID;
+// Plans the launch, checks the workspace and fills the fields both attention
+// entry points share; `a` holds the rest (q, or the RoPE prologue's inputs).
+static int run_attention(AttnArgs& a, const void* k, const void* v, const int64_t* position, int positions,
+                         void* out, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity, int64_t dim,
+                         double scale, void* workspace, int64_t workspace_bytes, const ftk_attn_config* cfg,
+                         bool rope, void* stream) {
+  if (!k || !v || !position || !out) return FTK_ERR_INVALID;
   if (positions != 1 && positions != batch) return FTK_ERR_INVALID;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return FTK_ERR_UNSUPPORTED;
+  if (!aligned16(k) || !aligned16(v) || !aligned16(out)) return FTK_ERR_UNSUPPORTED;
+  if (rope && cfg && cfg->kind && cfg->kind != FTK_ATTN_QUAD) return FTK_ERR_UNSUPPORTED;
   DeviceInfo d = device_info();
   if (!d.ok) return FTK_ERR_INVALID;
   ftk_attn_plan p;
   AttnShape shape;
   const int st = attn_plan(batch, q_heads, kv_heads, capacity, dim, d.cus, cfg, &p, &shape);
   if (st != FTK_OK) return st;
+  if (rope && p.kind != FTK_ATTN_QUAD) return FTK_ERR_UNSUPPORTED;
   float* partial = nullptr;
   float* stats = nullptr;
   if (p.splits > 1) {
@@ -796,8 +804,6 @@ int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const
     partial = (float*)workspace;
     stats = partial + (size_t)shape.groups * p.splits * shape.group_size * dim;
   }
-  AttnArgs a;
-  a.q = (const uint16_t*)q;
   a.k = (const uint16_t*)k;
   a.v = (const uint16_t*)v;
   a.position = position;
@@ -806,11 +812,50 @@ int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const
   a.partial = partial;
   a.stats = stats;
   a.kv_heads = (int)kv_heads;
+  a.q_heads = (int)q_heads;
   a.capacity = (int)capacity;
   a.splits = p.splits;
   a.chunk = p.chunk;
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   return hip_status(launch_attention(a, shape, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const int64_t* position,
+                              int positions, void* out, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                              int64_t capacity, int64_t dim, double scale, void* workspace, int64_t workspace_bytes,
+                              const ftk_attn_config* cfg, void* stream) {
+  if (!q) return FTK_ERR_INVALID;
+  if (!aligned16(q)) return FTK_ERR_UNSUPPORTED;
+  AttnArgs a{};
+  a.q = (const uint16_t*)q;
+  return run_attention(a, k, v, position, positions, out, batch, q_heads, kv_heads, capacity, dim, scale, workspace,
+                       workspace_bytes, cfg, false, stream);
+}
+
+int ftk_rope_decode_attention_bf16(const void* packed, const void* q_gain, const void* k_gain, float q_eps,
+                                   float k_eps, const void* cos, const void* sin, int64_t table_rows,
+                                   const int64_t* position, int positions, const int64_t* phases, void* keys,
+                                   void* values, void* out, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                   int64_t capacity, int64_t dim, double scale, void* workspace,
+                                   int64_t workspace_bytes, const ftk_attn_config* cfg, void* stream) {
+  if (!packed || !q_gain || !k_gain || !cos || !sin || table_rows < 1) return FTK_ERR_INVALID;
+  if (!aligned16(packed) || !aligned16(q_gain) || !aligned16(k_gain) || !aligned16(cos) || !aligned16(sin))
+    return FTK_ERR_UNSUPPORTED;
+  if (dim != 128) return FTK_ERR_UNSUPPORTED;
+  AttnArgs a{};
+  a.packed = (const uint16_t*)packed;
+  a.q_gain = (const uint16_t*)q_gain;
+  a.k_gain = (const uint16_t*)k_gain;
+  a.q_eps = q_eps;
+  a.k_eps = k_eps;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.table_rows = table_rows;
+  a.phases = phases;
+  a.k_store = (uint16_t*)keys;
+  a.v_store = (uint16_t*)values;
+  return run_attention(a, keys, values, position, positions, out, batch, q_heads, kv_heads, capacity, dim, scale,
+                       workspace, workspace_bytes, cfg, true, stream);
 }
 
 int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride, const void* q_gain,

@@ -149,6 +149,20 @@ struct AttnArgs {
   int capacity;             // cache slots per group
   int splits, chunk;        // slot intervals per group and slots per interval
   float scale_log2;         // scale * log2(e), formed in double
+  // Q/K head norm + RoPE in the QUAD kind's prologue (rope_attention): q is
+  // unused; query, key and value heads come from the packed QKV rows, and the
+  // split holding the row's own slot writes its key and value to k_store / v_store.
+  const uint16_t* packed;   // [rows, (Hq + 2 Hkv) D] BF16
+  const uint16_t* q_gain;   // [D]
+  const uint16_t* k_gain;   // [D]
+  const uint16_t* cos;      // [table_rows, D] BF16
+  const uint16_t* sin;
+  const int64_t* phases;    // [rows] RoPE phase added to the position, or null
+  uint16_t* k_store;        // the caches k, v as written
+  uint16_t* v_store;
+  int64_t table_rows;
+  int q_heads;
+  float q_eps, k_eps;
 };
 
 // Launch shape of the decode attention.

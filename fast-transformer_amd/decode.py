@@ -7,8 +7,8 @@ One step, per row b at its device-side position p_b:
 
   layer 0   qkv, r = embed_rms_norm_linear(ids, E, ln1, W_qkv)   embedding gather + norm + QKV, one launch
   layer l   qkv    = rms_norm_linear(r, ln1, W_qkv)               norm + QKV, one launch
-            q      = qk_rope_cache(qkv, ...)                      head norms + RoPE; K, V into slot p_b
-            a      = decode attention over slots 0..p_b
+            a      = rope_attend(qkv, ...)                        head norms + RoPE, K, V into slot p_b,
+                                                                  decode attention over slots 0..p_b
             r      = linear_residual(a, W_o, r)                   O, the residual add in its epilogue
             act    = gate_up_swiglu(r, W_gu, ln2)                 norm + gate/up + SwiGLU
             r      = linear_residual(act, W_down, r)              down, the residual add in its epilogue
@@ -17,9 +17,12 @@ One step, per row b at its device-side position p_b:
 The reference adds each sublayer's output to the residual stream in the next
 norm (add_rms_norm, decode.py:236-243, :258-261, :291-296); here the add runs
 in the epilogue of the projection that produces it, which stores the same BF16
-sum, so no norm prologue has to read a second [rows, H] stream. That is 6
-launches per layer (7 with a merge of attention splits) and one for the
-vocabulary. The weights are the model's own tensors (BF16, on the GPU),
+sum, so no norm prologue has to read a second [rows, H] stream. The head
+norms, RoPE and the cache update run in the attention kernel's prologue
+(rope_attend) where it takes the head layout (head_dim 128, at most 4 query
+heads per KV head; otherwise qk_rope_cache and decode attention launch
+apart). That is 5 launches per layer (6 with a merge of attention splits)
+and one for the vocabulary. The weights are the model's own tensors (BF16, on the GPU),
 packed once as the reference packs them ([Wq; Wk; Wv], [Wg; Wu],
 layers.py:23-26, :92-95). Positions, input ids and the RoPE phase live on the
 device, so one captured graph serves every step (``Decoder.capture``), the way
@@ -83,7 +86,7 @@ class Decoder:
     writes each layer's key and value at slot ``position[b]`` of row b.
     """
 
-    def __init__(self, model, batch, capacity):
+    def __init__(self, model, batch, capacity, fused_rope=True):
         base = model.model
         embed = base.embed_tokens.weight
         if embed.dtype != torch.bfloat16 or embed.device.type != "cuda":
@@ -105,6 +108,12 @@ class Decoder:
         self.position = torch.zeros((batch,), dtype=torch.int64, device=device)
         self.token_ids = torch.zeros((batch,), dtype=torch.int64, device=device)
         self._graph = None
+        first = self.layers[0]
+        gains = [t for layer in self.layers for t in (layer.q_norm.weight, layer.k_norm.weight)]
+        #: Head norms + RoPE in the attention launch (else the separate qk_rope_cache launch).
+        self.fused_rope = bool(fused_rope) and _attention.rope_attention_supported(
+            first.q_heads, self.cache.keys[0].shape[1], self.cache.keys[0].shape[3]) and \
+            all(t.is_contiguous() and t.data_ptr() % 16 == 0 for t in [self.cos, self.sin, self.cache.store, *gains])
 
     def step(self):
         """One decode token per row at ``position`` (engine/decode.py:215-297 for a one-token step)."""
@@ -118,10 +127,16 @@ class Decoder:
             else:
                 qkv = _linear.rms_norm_linear(residual, layer.input_norm.weight, eps, layer.qkv_weight)
             keys, values = self.cache.keys[index], self.cache.values[index]
-            query = _rope.qk_rope_cache(qkv.view(batch, 1, -1), layer.q_norm, layer.k_norm, self.cos, self.sin,
-                                        self.position, keys, values, layer.q_heads, rows=True, phases=self.phases)
-            attention = _attention.attend(query.reshape(batch, layer.q_heads, -1), keys, values, self.position,
-                                          layer.scaling)
+            if self.fused_rope:
+                attention = _attention.rope_attend(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin,
+                                                   self.position, keys, values, layer.q_heads, layer.scaling,
+                                                   phases=self.phases)
+            else:
+                query = _rope.qk_rope_cache(qkv.view(batch, 1, -1), layer.q_norm, layer.k_norm, self.cos, self.sin,
+                                            self.position, keys, values, layer.q_heads, rows=True,
+                                            phases=self.phases)
+                attention = _attention.attend(query.reshape(batch, layer.q_heads, -1), keys, values,
+                                              self.position, layer.scaling)
             residual = _linear.linear_residual(attention.view(batch, -1), layer.o_weight, residual)
             act = _swiglu.gate_up_swiglu(residual, layer.gate_up_weight, layer.post_norm.weight,
                                          layer.post_norm.variance_epsilon)

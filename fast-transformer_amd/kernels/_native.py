@@ -101,6 +101,10 @@ SIGNATURES = {
     "ftk_decode_attention_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p, _i64, _i64,
                                          _i64, _i64, _i64, ctypes.c_double, _c_void_p, _i64,
                                          ctypes.POINTER(AttnConfig), _c_void_p]),
+    "ftk_rope_decode_attention_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _float, _float, _c_void_p, _c_void_p,
+                                              _i64, _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                              _i64, _i64, _i64, _i64, _i64, ctypes.c_double, _c_void_p, _i64,
+                                              ctypes.POINTER(AttnConfig), _c_void_p]),
     "ftk_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(AttnConfig)]),
     "ftk_plan_decode_attention": (_int, [_i64, _i64, _i64, _i64, _i64, _int, ctypes.POINTER(AttnConfig),
                                          ctypes.POINTER(AttnPlan)]),

@@ -55,6 +55,68 @@ def attend(query, key, value, position, scale, config=None):
     return out
 
 
+#: Head dimension and query heads per KV head the fused RoPE prologue takes (the QUAD kind).
+ROPE_DIM, ROPE_MAX_GROUP = 128, 4
+
+
+def _aligned(*tensors):
+    return all(t.data_ptr() % 16 == 0 for t in tensors)
+
+
+def rope_attention_supported(query_heads, kv_heads, dim, config=None):
+    """Whether ``rope_attend`` takes this head layout: D = 128, at most 4 query heads per KV head."""
+    if config is not None and config.kind not in (0, _native.ATTN_QUAD):
+        return False
+    return dim == ROPE_DIM and query_heads % kv_heads == 0 and query_heads // kv_heads <= ROPE_MAX_GROUP
+
+
+def rope_attend(packed, q_norm, k_norm, cos, sin, position, keys, values, q_heads, scale, phases=None,
+                config=None):
+    """One decode token per row: qk_rope_cache (decode form) and decode_attention in one launch (plus the merge).
+
+    Replaces engine/layers.py:51-55 then :76 for a one-token step: packed
+    BF16 QKV [B, (Hq + 2 Hkv) D] (or [B, 1, ...]); q_norm / k_norm the head
+    norms; cos / sin whole BF16 tables [table_rows, D], row b rotated at
+    position[b] + phases[b] (``phases`` [B] or [B, 1] int64, or None for 0);
+    position int64 [1] or [B]. Writes row b's key and value heads into
+    ``keys`` / ``values`` [B, Hkv, C, D] at slot position[b] and returns the
+    attention output [B, 1, Hq, D] over slots 0..position[b]. The same
+    roundings as the two launches; FP32 sums in another order, so results
+    agree with them within a BF16 ulp. Needs ``rope_attention_supported``
+    and 16-byte aligned tensors (ValueError otherwise).
+    """
+    batch, kv_heads, capacity, dim = keys.shape
+    width = (q_heads + 2 * kv_heads) * dim
+    assert packed.dtype == keys.dtype == values.dtype == cos.dtype == sin.dtype == torch.bfloat16
+    assert packed.numel() == batch * width and packed.shape[0] == batch and packed.shape[-1] == width
+    assert packed.is_contiguous() and keys.is_contiguous() and values.is_contiguous()
+    assert values.shape == keys.shape
+    assert cos.shape == sin.shape and cos.shape[-1] == dim and cos.is_contiguous() and sin.is_contiguous()
+    assert position.dtype == torch.int64 and position.numel() in (1, batch)
+    if phases is not None:
+        assert phases.dtype == torch.int64 and phases.numel() == batch and phases.is_contiguous()
+    if not rope_attention_supported(q_heads, kv_heads, dim, config):
+        raise ValueError(f"the fused RoPE attention takes D = {ROPE_DIM} and at most {ROPE_MAX_GROUP} query heads "
+                         f"per KV head, got D = {dim}, {q_heads} / {kv_heads} heads")
+    q_weight, k_weight = q_norm.weight.contiguous(), k_norm.weight.contiguous()
+    _native.require_gpu(packed, keys, values, cos, sin, position, q_weight, k_weight)
+    if not _aligned(packed, keys, values, cos, sin, q_weight, k_weight):
+        raise ValueError("the fused RoPE attention needs 16-byte aligned tensors")
+    out = torch.empty((batch, 1, q_heads, dim), device=packed.device, dtype=packed.dtype)
+    cfg = ctypes.byref(config) if config is not None else None
+    need = int(_native.lib().ftk_decode_attention_workspace_bytes(batch, q_heads, kv_heads, capacity, dim, cfg))
+    if need < 0:
+        raise ValueError(f"decode attention does not take this shape: {tuple(keys.shape)} with {q_heads} heads")
+    ws = _native.workspace(packed.device, need, "attention") if need > 0 else None
+    _native.call("ftk_rope_decode_attention_bf16", _native.ptr(packed), _native.ptr(q_weight),
+                 _native.ptr(k_weight), float(q_norm.variance_epsilon), float(k_norm.variance_epsilon),
+                 _native.ptr(cos), _native.ptr(sin), cos.numel() // dim, _native.ptr(position), position.numel(),
+                 _native.ptr(phases), _native.ptr(keys), _native.ptr(values), _native.ptr(out), batch, q_heads,
+                 kv_heads, capacity, dim, float(scale), _native.ptr(ws), ws.numel() if ws is not None else 0, cfg,
+                 _native.stream_of(packed))
+    return out
+
+
 def block_attention(query, key, value, position, scale, chain):
     """Verify-block attention (engine/kernels/decode_attention.py:637-680): outside this library.
 

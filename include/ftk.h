@@ -265,6 +265,28 @@ int ftk_decode_attention_bf16(const void* q, const void* k, const void* v, const
                               void* out, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
                               int64_t dim, double scale, void* workspace, int64_t workspace_bytes,
                               const ftk_attn_config* cfg, void* stream);
+/* One-token decode attention that starts from the packed QKV rows: the Q/K head
+ * norm + RoPE + cache update of ftk_qk_rope_cache_bf16 (decode form: whole
+ * cos/sin tables [table_rows, D], row b rotates at position + phases[b], phases
+ * null = 0) runs in the attention kernel's prologue, then the attention of
+ * ftk_decode_attention_bf16 over slots 0..position. packed [B, (Hq + 2 Hkv) D]
+ * BF16; the key and value heads go to keys / values [B, Hkv, C, D] at slot
+ * position (when it lies in the cache), out [B, Hq, D]. Arithmetic and roundings
+ * are those of the two entry points; the order of FP32 sums differs, so results
+ * agree with the two-launch form within a BF16 ulp, not bit for bit. A phase
+ * outside the tables leaves that row's output unspecified and its slot
+ * unwritten. QUAD kind only: D = 128, Hq / Hkv <= 4, every pointer 16-byte
+ * aligned (else FTK_ERR_UNSUPPORTED, and the caller takes the two launches). The
+ * workspace is that of ftk_decode_attention_bf16 for the same shape and cfg.
+ * Replaces qk_rope_cache + decode_attention of a one-token decode step
+ * (engine/layers.py:51-55, :76; engine/kernels/qk_rope.py:97-129,
+ * engine/kernels/decode_attention.py:229-258). */
+int ftk_rope_decode_attention_bf16(const void* packed, const void* q_gain, const void* k_gain, float q_eps,
+                                   float k_eps, const void* cos, const void* sin, int64_t table_rows,
+                                   const int64_t* position, int positions, const int64_t* phases, void* keys,
+                                   void* values, void* out, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                   int64_t capacity, int64_t dim, double scale, void* workspace,
+                                   int64_t workspace_bytes, const ftk_attn_config* cfg, void* stream);
 /* Workspace bytes of that call on the current device (-1: invalid shape or no device). */
 int64_t ftk_decode_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity,
                                              int64_t dim, const ftk_attn_config* cfg);

@@ -81,6 +81,55 @@ def test_unsupported_shapes_rejected():
         _native.FTK_ERR_UNSUPPORTED  # 16-byte alignment
 
 
+def test_quad_needs_32_bit_cache_offsets():
+    """QUAD addresses one (row, KV head) cache in 32-bit bytes: longer caches take ROWS."""
+    out = _native.AttnPlan()
+    assert plan(1, 32, 8, 16_000_000, 128).kind == _native.ATTN_QUAD
+    assert plan(1, 32, 8, 1 << 24, 128).kind == _native.ATTN_ROWS
+    quad = _native.AttnConfig(_native.ATTN_QUAD, 0, 0, 0)
+    assert _native.lib().ftk_plan_decode_attention(1, 32, 8, 1 << 24, 128, 256, ctypes.byref(quad),
+                                                   ctypes.byref(out)) == _native.FTK_ERR_UNSUPPORTED
+
+
+def test_rope_entry_rejects_before_any_launch():
+    call = _native.lib().ftk_rope_decode_attention_bf16
+    f = ctypes.c_void_p(256)
+
+    def run(packed=f, gain=f, cos=f, table=64, pos=f, positions=1, keys=f, out=f, b=1, hq=32, d=128, cfg=None):
+        return call(packed, gain, gain, 1e-6, 1e-6, cos, cos, table, pos, positions, None, keys, keys, out, b, hq,
+                    8, 64, d, 0.1, None, 0, cfg, None)
+
+    assert run(packed=None) == _native.FTK_ERR_INVALID
+    assert run(gain=None) == _native.FTK_ERR_INVALID
+    assert run(table=0) == _native.FTK_ERR_INVALID
+    assert run(pos=None) == _native.FTK_ERR_INVALID
+    assert run(positions=2) == _native.FTK_ERR_INVALID  # 1 or the batch
+    assert run(packed=ctypes.c_void_p(258)) == _native.FTK_ERR_UNSUPPORTED  # 16-byte alignment
+    assert run(cos=ctypes.c_void_p(264)) == _native.FTK_ERR_UNSUPPORTED
+    assert run(d=64) == _native.FTK_ERR_UNSUPPORTED  # QUAD only
+    rows = _native.AttnConfig(_native.ATTN_ROWS, 0, 0, 0)
+    assert run(cfg=ctypes.byref(rows)) == _native.FTK_ERR_UNSUPPORTED
+
+
+def test_rope_wrapper_support_and_no_cpu_path():
+    assert A.rope_attention_supported(32, 8, 128) and A.rope_attention_supported(8, 8, 128)
+    assert not A.rope_attention_supported(40, 8, 128)  # five query heads per KV head
+    assert not A.rope_attention_supported(32, 8, 64)
+    assert not A.rope_attention_supported(32, 8, 128, _native.AttnConfig(_native.ATTN_ROWS, 0, 0, 0))
+
+    class Norm:
+        weight, variance_epsilon = torch.ones(128, dtype=torch.bfloat16), 1e-6
+
+    k = torch.zeros(1, 8, 16, 128, dtype=torch.bfloat16)
+    table = torch.zeros(16, 128, dtype=torch.bfloat16)
+    packed = torch.zeros(1, 48 * 128, dtype=torch.bfloat16)
+    pos = torch.zeros(1, dtype=torch.int64)
+    with pytest.raises(ValueError, match="GPU"):
+        A.rope_attend(packed, Norm, Norm, table, table, pos, k, k.clone(), 32, 0.1)
+    with pytest.raises(AssertionError):
+        A.rope_attend(packed[:, :-128], Norm, Norm, table, table, pos, k, k.clone(), 32, 0.1)  # width
+
+
 def _args(b=1, hq=8, hkv=2, c=16, d=64, t=1):
     q = torch.zeros(b, hq, t, d, dtype=torch.bfloat16)
     k = torch.zeros(b, hkv, c, d, dtype=torch.bfloat16)

@@ -38,12 +38,14 @@ BARS = {Q.SMALL: ((2e-2, 1e-2), (2e-2, 1e-2)), Q.QWEN3_06B: ((2e-2, 1e-2), (2e-2
         Q.QWEN3_8B: ((5e-2, 2e-2), (0.1, 2e-2))}
 
 
-@pytest.mark.parametrize("dims,batch", [(Q.SMALL, 1), (Q.SMALL, 2), (Q.QWEN3_06B, 1), (Q.QWEN3_06B, 4),
-                                        (Q.QWEN3_8B, 2)])
-def test_generate_matches_oracle_and_transformers(cuda, dims, batch):
+@pytest.mark.parametrize("dims,batch,fused", [(Q.SMALL, 1, True), (Q.SMALL, 2, True), (Q.SMALL, 2, False),
+                                              (Q.QWEN3_06B, 1, True), (Q.QWEN3_06B, 4, True),
+                                              (Q.QWEN3_8B, 2, True)])
+def test_generate_matches_oracle_and_transformers(cuda, dims, batch, fused):
     capacity, steps = 24, 5
     m, gpu, prompt = _setup(dims, batch, capacity)
-    dec = D.Decoder(gpu, batch, capacity)
+    dec = D.Decoder(gpu, batch, capacity, fused_rope=fused)
+    assert dec.fused_rope == fused
     ids, logits = dec.generate(prompt, steps)
     torch.cuda.synchronize()
     length = prompt.shape[1]
@@ -85,3 +87,25 @@ def test_graph_replays_give_the_eager_bits(cuda, batch):
     again_ids, again_logits = graphed.generate(prompt, steps, graph=True)
     torch.cuda.synchronize()
     assert torch.equal(again_ids, e_ids) and torch.equal(again_logits, e_logits)
+
+
+@pytest.mark.parametrize("dims,batch", [(Q.SMALL, 2), (Q.QWEN3_8B, 1)])
+def test_rope_in_the_attention_launch_matches_the_two_launches(cuda, dims, batch):
+    """The head norms + RoPE in the attention prologue against the separate qk_rope_cache launch."""
+    capacity, steps = 24, 5
+    _, gpu, prompt = _setup(dims, batch, capacity, seed=11)
+    fused = D.Decoder(gpu, batch, capacity)
+    apart = D.Decoder(gpu, batch, capacity, fused_rope=False)
+    assert fused.fused_rope and not apart.fused_rope
+    f_ids, f_logits = fused.generate(prompt, steps)
+    a_ids, a_logits = apart.generate(prompt, steps)
+    torch.cuda.synchronize()
+    (oa, orl), _ = BARS[dims]
+    want = bf16.to_f32(to_bits(a_logits))
+    assert Q.close(bf16.to_f32(to_bits(f_logits)), want, oa, orl)
+    ok, checked = Q.clear_ids_agree(f_ids.cpu().numpy(), want[:, prompt.shape[1] - 1:], margin=2.5 * oa)
+    assert ok and checked >= batch * steps // 2
+    n = prompt.shape[1] + steps - 1
+    k_f = bf16.to_f32(to_bits(fused.cache.store[:, :, :, :, :n]))
+    k_a = bf16.to_f32(to_bits(apart.cache.store[:, :, :, :, :n]))
+    assert Q.close(k_f, k_a, oa, orl)
