@@ -5,7 +5,7 @@ named after (include/ftk.h, through ``kernels._native``), so eager results
 are identical. A fake (meta) implementation gives the output shapes without
 running anything, so the ops trace under ``torch.compile`` / ``torch.export``
 and take part in FakeTensor shape propagation. Mutated arguments are declared
-(``qk_rope_cache`` writes the KV caches in place).
+(``qk_rope_cache`` and ``rope_attend`` write the KV caches in place).
 
     import kernels.ops  # registers the ops
     y = torch.ops.ftk.rms_norm_linear(x, gamma, 1e-6, w)
@@ -24,6 +24,8 @@ Registered:
   ftk::decode_attention(query, key, value, position, scale) decode_attention.py:229-258
   ftk::qk_rope_cache(packed, q_weight, k_weight, q_eps, k_eps, cos, sin, position, keys!, values!, q_heads)
                                                             qk_rope.py:97-129 (one decode step)
+  ftk::rope_attend(packed, q_weight, k_weight, q_eps, k_eps, cos, sin, position, keys!, values!, q_heads, scale,
+                   phases?)                                 both of the above in one launch (layers.py:51-55, :76)
 """
 
 from typing import Optional, Tuple
@@ -170,3 +172,16 @@ def qk_rope_cache(packed: Tensor, q_weight: Tensor, k_weight: Tensor, q_eps: flo
 def _(packed, q_weight, k_weight, q_eps, k_eps, cos, sin, position, keys, values, q_heads):
     batch, tokens = packed.shape[:2]
     return packed.new_empty((batch, tokens, q_heads, keys.shape[-1]), dtype=keys.dtype)
+
+
+@torch.library.custom_op("ftk::rope_attend", mutates_args=("keys", "values"))
+def rope_attend(packed: Tensor, q_weight: Tensor, k_weight: Tensor, q_eps: float, k_eps: float, cos: Tensor,
+                sin: Tensor, position: Tensor, keys: Tensor, values: Tensor, q_heads: int, scale: float,
+                phases: Optional[Tensor] = None) -> Tensor:
+    return _attention.rope_attend(packed, _Norm(q_weight, q_eps), _Norm(k_weight, k_eps), cos, sin, position, keys,
+                                  values, q_heads, scale, phases=phases)
+
+
+@rope_attend.register_fake
+def _(packed, q_weight, k_weight, q_eps, k_eps, cos, sin, position, keys, values, q_heads, scale, phases=None):
+    return packed.new_empty((packed.shape[0], 1, q_heads, keys.shape[-1]), dtype=keys.dtype)

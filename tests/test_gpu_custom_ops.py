@@ -35,6 +35,18 @@ def test_ops_equal_the_functions(cuda):
     pos = torch.tensor([80], device=cuda, dtype=torch.int64)
     assert torch.equal(torch.ops.ftk.decode_attention(q, k, v, pos, 128 ** -0.5),
                        DA.decode_attention(q, k, v, pos, 128 ** -0.5))
+    packed = seeded((1, 32 * 128), seed=8, device=cuda)
+    gq, gk = seeded((128,), seed=9, scale=0.1, shift=1.0, device=cuda), seeded((128,), seed=10, device=cuda)
+    cos, sin = seeded((96, 128), seed=11, device=cuda), seeded((96, 128), seed=12, device=cuda)
+    k2, v2 = k.clone(), v.clone()
+    got = torch.ops.ftk.rope_attend(packed, gq, gk, 1e-6, 1e-6, cos, sin, pos, k, v, 16, 128 ** -0.5)
+
+    class Norm:
+        def __init__(self, weight):
+            self.weight, self.variance_epsilon = weight, 1e-6
+
+    want = DA.rope_attend(packed, Norm(gq), Norm(gk), cos, sin, pos, k2, v2, 16, 128 ** -0.5)
+    assert torch.equal(got, want) and torch.equal(k, k2) and torch.equal(v, v2)
 
 
 def test_opcheck_schema_and_fake(cuda):

@@ -7,7 +7,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 import kernels.ops  # noqa: F401  (registers torch.ops.ftk.*)
 
 NAMES = ("linear", "linear_residual", "rms_norm_linear", "add_rms_norm_linear", "gate_up_swiglu", "lm_head_argmax", "rms_norm",
-         "add_rms_norm", "swiglu", "argmax", "decode_attention", "qk_rope_cache")
+         "add_rms_norm", "swiglu", "argmax", "decode_attention", "qk_rope_cache", "rope_attend")
 
 
 def test_every_op_is_registered():
@@ -43,3 +43,7 @@ def test_fake_shapes():
                                              1e-6, torch.empty(1, 1, 128, dtype=bf), torch.empty(1, 1, 128, dtype=bf),
                                              pos, cache, torch.empty_like(cache), 32)
         assert rope_q.shape == (2, 1, 32, 128)
+        table = torch.empty(64, 128, dtype=bf)
+        out = torch.ops.ftk.rope_attend(packed.view(2, -1), torch.empty(128, dtype=bf), torch.empty(128, dtype=bf),
+                                        1e-6, 1e-6, table, table, pos, cache, torch.empty_like(cache), 32, 0.088)
+        assert out.shape == (2, 1, 32, 128)
