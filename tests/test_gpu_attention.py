@@ -91,7 +91,7 @@ def test_reference_cases_match_oracle_and_sdpa(cuda, batch, kv_heads, dim, capac
     assert np.all(np.abs(g - want_exact) <= 0.03125 + 0.01 * np.abs(want_exact))
 
 
-@pytest.mark.parametrize("splits", [1, 2, 7, 64])
+@pytest.mark.parametrize("splits", [1, 2, 7, 64, 256, 500])
 @pytest.mark.parametrize("kind,waves,unroll", [(_native.ATTN_ROWS, 4, 2), (_native.ATTN_ROWS, 4, 4),
                                                (_native.ATTN_ROWS, 8, 2), (_native.ATTN_ROWS, 8, 4),
                                                (_native.ATTN_ROWS, 4, 8), (_native.ATTN_QUAD, 4, 1),
