@@ -586,7 +586,8 @@ def decode_model_table(cfg, dev, context=FULL_LAYER_CONTEXT):
 
 
 def attention_table(cfg, dev):
-    """µs / GB/s / fraction of the HBM roofline of decode_attention over full caches (all slots valid)."""
+    """µs / GB/s / fraction of the HBM roofline of decode_attention over full caches (all slots valid),
+    and of rope_attend (QK norm + RoPE + the cache write of the last slot in the attention's prologue)."""
     out = {}
     hq, hkv, d = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
     for b, c, copies in ATTN_CASES:
@@ -599,6 +600,16 @@ def attention_table(cfg, dev):
         us = time_graph(graph) / copies
         byts = 2 * b * hkv * c * d * 2 + 2 * 2 * b * hq * d
         out[f"attention 8B decode B={b} C={c}"] = shape_entry(us, byts)
+        del graph
+        packed = torch.randn((b, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
+        gain = _Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS)
+        table = torch.randn((c, d), generator=g, device=dev).to(torch.bfloat16)
+        graph = capture(lambda: [DA.rope_attend(packed, gain, gain, table, table, pos, k, v, hq, d ** -0.5)
+                                 for k, v in zip(ks, vs)])
+        us = time_graph(graph) / copies
+        byts = 2 * b * hkv * (c - 1) * d * 2 + b * (hq + 2 * hkv) * d * 2 + 2 * b * hkv * d * 2 + 2 * b * hq * d
+        out[f"attention 8B decode B={b} C={c}, QK norm + RoPE + cache write in the prologue"] = \
+            shape_entry(us, byts)
         del ks, vs, graph
         stage(f"attention B={b} C={c} done")
     return out
