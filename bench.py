@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-shapes]
 
-One step = one M=1 decode step's projections at Qwen3-8B shapes (BASELINE
+One step = one M=1 decode step's projections at Qwen3-8B shapes (BASELINE.json
 config 3): 36 layers, each RMSNorm-prologue QKV 4096->6144, O 4096->4096,
 RMSNorm-prologue gate/up 4096->2x12288 with the SwiGLU epilogue, down
 12288->4096, every layer with its own weights (13.9 GB resident in HBM), then
@@ -15,7 +15,7 @@ value = algorithmic bytes of the step / step time (GB/s). Rank 0 prints one
 JSON line with the contract fields plus ``roofline`` (dominant kernel: the
 fused gate/up + SwiGLU GEMV), ``cpu_baseline`` (the reference's torch CPU path on
 a bounded sample of the same workload) and ``per_shape`` (µs, GB/s and fraction
-of the 8 TB/s HBM roofline for every BASELINE configuration, plus the split-KV
+of the 8 TB/s HBM roofline for every BASELINE.json configuration, plus the split-KV
 decode attention at Qwen3-8B heads, a whole decode layer and a whole greedy decode
 step of a Qwen3-8B-shape transformers model through decode.py).
 """
@@ -404,7 +404,7 @@ C5_COPIES = 4
 
 
 def shapes_table(model8, step8, dev):
-    """µs / GB/s / fraction of the HBM roofline for every BASELINE configuration (C1-C5)."""
+    """µs / GB/s / fraction of the HBM roofline for every BASELINE.json configuration (C1-C5)."""
     out = {}
     cfg = model8.cfg
     lb = layer_bytes(cfg, 1)

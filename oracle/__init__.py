@@ -20,7 +20,7 @@ How each function is pinned (independent checks, in tests/test_oracle.py):
   path.project           -- fp64 exact product: <= 0.75 BF16 ulp (the
                             reference's bar, agent/local_cpu/interp/
                             run_numeric.py:59-61); torch CPU F.linear within
-                            BASELINE tolerance; integer-valued inputs whose
+                            the 2e-2 + 1e-2|ref| bar; integer-valued inputs whose
                             product is exact must match bit for bit.
   path.rms_norm          -- transformers' Qwen3RMSNorm (library routine):
                             >= 99.9% bit-equal, <= 2 ulp; the wrong-cast

@@ -83,7 +83,7 @@ def oracle_run(decode, w, cfg, tokens, batch, capacity, layers):
 
 
 def close(got, want, atol=2e-2, rtol=1e-2):
-    """|got - want| <= atol + rtol |want| everywhere (BASELINE's elementwise bar)."""
+    """|got - want| <= atol + rtol |want| everywhere (the path's elementwise bar)."""
     return bool(np.all(np.abs(np.asarray(got, np.float64) - want) <= atol + rtol * np.abs(want)))
 
 

@@ -2,7 +2,7 @@
 
 Bars: <= 0.75 BF16 ulp of the fp64 product at the reference's own test shapes
 (agent/local_cpu/interp/run_numeric.py:46-62), and |y - ref| <= 2e-2 + 1e-2|ref|
-(BASELINE tolerance, rel 1e-2 / abs 2e-2) against the oracle and torch's
+(rel 1e-2 / abs 2e-2) against the oracle and torch's
 F.linear at the model shapes. Launch shapes that only reorder the same FP32
 sums must agree bit for bit.
 """

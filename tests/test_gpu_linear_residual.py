@@ -5,7 +5,7 @@ add_rms_norm (engine/kernels/rmsnorm.py:86-95) applied to the projection's outpu
 - bit for bit the kernel's own projection (same launch choice) followed by that add,
   for every kind (STREAM, QUAD, STAGE, MFMA_STREAM, GEMV, MFMA, generic), row counts
   1..32 and ragged N;
-- within BASELINE's bar of the oracle's projection followed by the same add;
+- within 2e-2 + 1e-2|ref| of the oracle's projection followed by the same add;
 - add_rms_norm's `summed` bit for bit (the standalone kernel on the projection's output);
 - in place (y = residual) through the C ABI, and in a replayed graph.
 """

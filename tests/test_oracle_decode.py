@@ -3,7 +3,7 @@
 Same BF16-valued weights; the oracle's prompt goes through one step per token
 and its greedy tokens are appended, then the library model evaluates the whole
 sequence at once. The oracle rounds to BF16 where the path does, so its logits
-sit within BASELINE's bar (|d| <= 2e-2 + 1e-2 |ref|) of the float32 ones, and
+sit within |d| <= 2e-2 + 1e-2 |ref| of the float32 ones, and
 its greedy ids equal theirs wherever the float32 top-2 gap is clear of that
 bar. Its caches hold the library's keys (after q/k norm and RoPE) and values.
 A wrong head mapping (each query head reading the other KV head of its pair)
