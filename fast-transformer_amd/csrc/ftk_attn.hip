@@ -397,8 +397,6 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
       vr[g][u] = buffer_load16(vrs, at(wave, g, u));
     }
   if constexpr (ROPE) {
-    // Keep the cache loads above: the head arithmetic waits for the head loads only.
-    __builtin_amdgcn_sched_barrier(0);
     qv = quad_head_rope(xq, gq, cs, sn, a.q_eps, lane);
     if (i4 >= G) qv = zero;
     if (own) {
