@@ -316,7 +316,11 @@ __device__ __forceinline__ u32x4_t quad_head_rope(u32x4_t x, u32x4_t g, u32x4_t 
 // packed row too: it writes them to the cache, reads only the slots before
 // it from memory, and starts wave 0's softmax state with the new slot
 // (score s, p = 1). No other workgroup of the launch reads that slot.
-template <int G, int W, int NG, bool ROPE>
+// FENCE (with ROPE): the head arithmetic is kept behind the first cache loads,
+// so it waits for the head loads only. That shortens a short split (the prologue
+// is most of it); in a long one the new slot's stores, then in flight ahead of
+// the loop, make the loop's waits drain more, so long splits go without.
+template <int G, int W, int NG, bool ROPE, bool FENCE = false>
 __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
   constexpr int D = 128, SLOTS = 16 * NG;  // a unit: NG groups of 16 cache rows
   __shared__ float p_lds[W][64];
@@ -397,6 +401,7 @@ __global__ __launch_bounds__(64 * W) void attn_quad_kernel(AttnArgs a) {
       vr[g][u] = buffer_load16(vrs, at(wave, g, u));
     }
   if constexpr (ROPE) {
+    if constexpr (FENCE) __builtin_amdgcn_sched_barrier(0);
     qv = quad_head_rope(xq, gq, cs, sn, a.q_eps, lane);
     if (i4 >= G) qv = zero;
     if (own) {
@@ -654,32 +659,37 @@ static hipError_t launch_for_dim(const AttnArgs& a, const AttnShape& s, hipStrea
   }
 }
 
-template <int G, bool ROPE>
+template <int G, bool ROPE, bool FENCE>
 static hipError_t launch_quad_for_group(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
   const dim3 grid((unsigned)(s.groups * s.splits));
   if (s.waves == 4 && s.unroll == 1)
-    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 1, ROPE>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 1, ROPE, FENCE>), grid, dim3(256), 0, stream, a);
   else if (s.waves == 4 && s.unroll == 2)
-    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 2, ROPE>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_quad_kernel<G, 4, 2, ROPE, FENCE>), grid, dim3(256), 0, stream, a);
   else if (s.waves == 8 && s.unroll == 1)
-    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 1, ROPE>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 1, ROPE, FENCE>), grid, dim3(512), 0, stream, a);
   else if (s.waves == 8 && s.unroll == 2)
-    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 2, ROPE>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((attn_quad_kernel<G, 8, 2, ROPE, FENCE>), grid, dim3(512), 0, stream, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
-template <bool ROPE>
+template <bool ROPE, bool FENCE>
 static hipError_t launch_quad(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
   switch (s.group_size) {
-    case 1: return launch_quad_for_group<1, ROPE>(a, s, stream);
-    case 2: return launch_quad_for_group<2, ROPE>(a, s, stream);
-    case 3: return launch_quad_for_group<3, ROPE>(a, s, stream);
-    case 4: return launch_quad_for_group<4, ROPE>(a, s, stream);
+    case 1: return launch_quad_for_group<1, ROPE, FENCE>(a, s, stream);
+    case 2: return launch_quad_for_group<2, ROPE, FENCE>(a, s, stream);
+    case 3: return launch_quad_for_group<3, ROPE, FENCE>(a, s, stream);
+    case 4: return launch_quad_for_group<4, ROPE, FENCE>(a, s, stream);
     default: return hipErrorInvalidValue;
   }
 }
+
+// Splits of up to this many slots take the RoPE prologue with the scheduling fence
+// (measured on MI355X: B = 1 x 4K slots in 128-slot splits gains ~1 us with it;
+// 1024- and 2048-slot splits lose 1-3.5 us).
+constexpr int kAttnFenceMaxChunk = 256;
 
 bool attn_supported(int kind, int dim, int group_size, int waves, int unroll) {
   if (waves != 4 && waves != 8) return false;
@@ -694,8 +704,10 @@ bool attn_supported(int kind, int dim, int group_size, int waves, int unroll) {
 hipError_t launch_attention(const AttnArgs& a, const AttnShape& s, hipStream_t stream) {
   // The head norm + RoPE prologue exists for the QUAD kind only (the caller checks).
   if (a.packed != nullptr && s.kind != FTK_ATTN_QUAD) return hipErrorInvalidValue;
-  hipError_t e = s.kind == FTK_ATTN_QUAD ? (a.packed != nullptr ? launch_quad<true>(a, s, stream)
-                                                                 : launch_quad<false>(a, s, stream))
+  const bool rope = a.packed != nullptr, fence = s.chunk <= kAttnFenceMaxChunk;
+  hipError_t e = s.kind == FTK_ATTN_QUAD ? (!rope   ? launch_quad<false, false>(a, s, stream)
+                                            : fence ? launch_quad<true, true>(a, s, stream)
+                                                    : launch_quad<true, false>(a, s, stream))
                  : s.dim == 128          ? launch_for_dim<128>(a, s, stream)
                                          : launch_for_dim<64>(a, s, stream);
   if (e != hipSuccess || s.splits == 1) return e;
