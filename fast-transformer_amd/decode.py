@@ -112,7 +112,7 @@ class Decoder:
         gains = [t for layer in self.layers for t in (layer.q_norm.weight, layer.k_norm.weight)]
         #: Head norms + RoPE in the attention launch (else the separate qk_rope_cache launch).
         self.fused_rope = bool(fused_rope) and _attention.rope_attention_supported(
-            first.q_heads, self.cache.keys[0].shape[1], self.cache.keys[0].shape[3]) and \
+            first.q_heads, self.cache.keys[0].shape[1], self.cache.keys[0].shape[3], capacity=capacity) and \
             all(t.is_contiguous() and t.data_ptr() % 16 == 0 for t in [self.cos, self.sin, self.cache.store, *gains])
 
     def step(self):

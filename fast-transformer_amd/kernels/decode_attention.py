@@ -63,9 +63,12 @@ def _aligned(*tensors):
     return all(t.data_ptr() % 16 == 0 for t in tensors)
 
 
-def rope_attention_supported(query_heads, kv_heads, dim, config=None):
-    """Whether ``rope_attend`` takes this head layout: D = 128, at most 4 query heads per KV head."""
+def rope_attention_supported(query_heads, kv_heads, dim, config=None, capacity=None):
+    """Whether ``rope_attend`` takes this head layout: D = 128, at most 4 query heads per KV head, and
+    (when given) a cache whose byte offsets fit 32 bits (up to 2^32 / 256 - 512 slots)."""
     if config is not None and config.kind not in (0, _native.ATTN_QUAD):
+        return False
+    if capacity is not None and (capacity + 512) * dim * 2 > 0xFFFFFFFF:
         return False
     return dim == ROPE_DIM and query_heads % kv_heads == 0 and query_heads // kv_heads <= ROPE_MAX_GROUP
 
@@ -95,7 +98,7 @@ def rope_attend(packed, q_norm, k_norm, cos, sin, position, keys, values, q_head
     assert position.dtype == torch.int64 and position.numel() in (1, batch)
     if phases is not None:
         assert phases.dtype == torch.int64 and phases.numel() == batch and phases.is_contiguous()
-    if not rope_attention_supported(q_heads, kv_heads, dim, config):
+    if not rope_attention_supported(q_heads, kv_heads, dim, config, capacity):
         raise ValueError(f"the fused RoPE attention takes D = {ROPE_DIM} and at most {ROPE_MAX_GROUP} query heads "
                          f"per KV head, got D = {dim}, {q_heads} / {kv_heads} heads")
     q_weight, k_weight = q_norm.weight.contiguous(), k_norm.weight.contiguous()

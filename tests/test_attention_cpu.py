@@ -116,6 +116,8 @@ def test_rope_wrapper_support_and_no_cpu_path():
     assert not A.rope_attention_supported(40, 8, 128)  # five query heads per KV head
     assert not A.rope_attention_supported(32, 8, 64)
     assert not A.rope_attention_supported(32, 8, 128, _native.AttnConfig(_native.ATTN_ROWS, 0, 0, 0))
+    assert A.rope_attention_supported(32, 8, 128, capacity=16_000_000)
+    assert not A.rope_attention_supported(32, 8, 128, capacity=1 << 24)  # QUAD's 32-bit offsets
 
     class Norm:
         weight, variance_epsilon = torch.ones(128, dtype=torch.bfloat16), 1e-6
