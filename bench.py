@@ -468,7 +468,9 @@ ATTN_CASES = ((1, 4096, 36), (1, 32768, 8), (16, 4096, 4))
 
 
 def profile_attention(cfg, dev, passes):
-    """Eager decode-attention launches over every ATTN_CASES cache set (for rocprofv3), then a 1 GiB copy."""
+    """Eager decode-attention launches over every ATTN_CASES cache set (for rocprofv3): per case,
+    ``passes`` passes of decode_attention, then as many of rope_attend (the QK norm + RoPE prologue);
+    then a 1 GiB copy."""
     hq, hkv, d = cfg["q_heads"], cfg["kv_heads"], cfg["head_dim"]
     for b, c, copies in ATTN_CASES:
         g = torch.Generator(device=dev).manual_seed(11)
@@ -479,6 +481,12 @@ def profile_attention(cfg, dev, passes):
         for _ in range(passes):
             for k, v in zip(ks, vs):
                 DA.decode_attention(q, k, v, pos, d ** -0.5)
+        packed = torch.randn((b, (hq + 2 * hkv) * d), generator=g, device=dev).to(torch.bfloat16)
+        gain = _Norm((1 + 0.1 * torch.randn((d,), generator=g, device=dev)).to(torch.bfloat16), EPS)
+        table = torch.randn((c, d), generator=g, device=dev).to(torch.bfloat16)
+        for _ in range(passes):
+            for k, v in zip(ks, vs):
+                DA.rope_attend(packed, gain, gain, table, table, pos, k, v, hq, d ** -0.5)
         torch.cuda.synchronize()
         stage(f"attention B={b} C={c}: {passes} passes over {copies} caches")
         del ks, vs
