@@ -267,8 +267,8 @@ def main():
                     help="profiling mode: only PASSES eager passes of the 36 gate/up + SwiGLU launches, "
                          "then one 1 GiB device copy as the counter reference")
     ap.add_argument("--profile-attention", type=int, default=0, metavar="PASSES",
-                    help="profiling mode: PASSES eager passes of decode attention over each ATTN_CASES cache set "
-                         "(distinct caches), then one 1 GiB device copy as the counter reference")
+                    help="profiling mode: PASSES eager passes of decode attention, then of rope_attend, over each "
+                         "ATTN_CASES cache set (distinct caches), then one 1 GiB device copy as the counter reference")
     ap.add_argument("--profile-rows", type=str, default="", metavar="M[,M...]",
                     help="profiling mode: two eager passes of the 36-layer projection chain at each M rows "
                          "(the C4 workload), then one 1 GiB device copy as the counter reference")
