@@ -141,11 +141,15 @@ class Step:
 
     def run(self):
         h = self.layers()
-        return A.lm_head_argmax(h, self.model.head, self.model.final_norm, EPS, logits=True, top=self.top)
+        return A.lm_head_argmax(h, self.model.head, self.model.final_norm, EPS, logits=True, top=self.top,
+                                ids_dtype=torch.int32)
 
 
 def capture(fn, warm=2):
-    """Warm ``fn`` eagerly (selection, workspaces), then capture it into a graph on a side stream."""
+    """Warm ``fn`` eagerly (selection, workspaces), then capture it into a graph on a side stream.
+
+    ``warm=0`` captures without running anything first (for calls that need no workspace or
+    selection), so that every launch of the kernels a profiler sees comes from graph replays."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -184,7 +188,7 @@ def shape_entry(us, byts, flops=None):
     return e
 
 
-def per_kind(step, kind):
+def per_kind(step, kind, warm=2):
     """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch."""
     def fn():
         for lw in step.model.layers:
@@ -198,29 +202,105 @@ def per_kind(step, kind):
                 L.linear(step.act_in, lw["down"])
     if kind == "down":
         step.act_in = torch.randn((step.m, step.model.cfg["inter"]), device=step.h.device).to(torch.bfloat16)
-    graph = capture(fn)
+    if warm == 0:
+        # no eager call before capture: size the shared workspace here (an allocation, no launch)
+        cfg = step.model.cfg
+        _native.project_workspace(step.h.device, step.m, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU,
+                                  prologue=True)
+    graph = capture(fn, warm)
     return time_graph(graph) / len(step.model.layers)
 
 
-def cpu_baseline(model, step, budget_s):
-    """The reference's torch-CPU path (BF16 F.linear + native-cast norm/SwiGLU) on a bounded sample.
+def roofline(step):
+    """The ``roofline`` object: the dominant kernel, the fused gate/up + SwiGLU GEMV (201 MB per launch
+    at M=1), timed over graph replays of its 36 launches (distinct weights). The graph is captured
+    without eager launches, so a kernel trace of ``bench.py --roofline-only`` holds replays only."""
+    cfg = step.model.cfg
+    gu_us = per_kind(step, "gate_up", warm=0)
+    gu_bytes = layer_bytes(cfg, 1)["gate_up"]
+    return {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
+            "kernel": kernel_name(L.plan(1, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU), True,
+                                  "SWIGLU") + " (Qwen3-8B gate/up 4096->2x12288, M=1)",
+            "avg_launch_us": round(gu_us, 3)}
 
-    Sample: the first two of the 36 layers at M=1, repeated until ~budget_s of CPU work.
-    """
+
+def cpu_share():
+    """(threads, how they were counted) for the CPU baseline: the cgroup CPU quota when one is set
+    (the box's share of the host), else the CPUs this process may run on, else os.cpu_count()."""
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if quota != "max":
+            return max(1, int(quota) // int(period)), "cgroup cpu.max quota"
+    except (OSError, ValueError):
+        pass
+    try:
+        return len(os.sched_getaffinity(0)), "sched_getaffinity"
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1, "os.cpu_count()"
+
+
+def _cpu_median(fn, seconds, max_reps=200):
+    """Median wall time (µs) of ``fn`` after one warm call, repeated for about ``seconds``."""
+    fn()
+    times, t_end = [], time.monotonic() + seconds
+    while (time.monotonic() < t_end or len(times) < 5) and len(times) < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e6, len(times)
+
+
+def cpu_baseline(model8, dev, budget_s):
+    """The reference's torch-CPU path (BF16 F.linear + native-cast norm / SwiGLU + torch.argmax,
+    oracle/torch_cpu.py) on the same seeded weights and inputs as the GPU run, for every BASELINE.json
+    configuration, on a bounded sample: C1 per call; C2 per layer over 4 of the 28 Qwen3-0.6B-shape
+    layers; C3 and C4 (M = 5, 8, 16) per layer over 2 of the 36 Qwen3-8B-shape layers; C5 per call.
+    Each figure is the median of repeated passes over about budget_s / 8 seconds."""
     from oracle import torch_cpu
 
-    threads = torch.get_num_threads()  # the host's CPU share (OMP_NUM_THREADS)
-    layers = [{k: v.cpu() for k, v in model.layers[i].items()} for i in range(2)]
-    h, attn = step.h.cpu(), step.attn.cpu()
-    torch_cpu.layer_projections(h, attn, layers[0], EPS)  # warm
-    times, t_end = [], time.monotonic() + budget_s
-    while time.monotonic() < t_end and len(times) < 50:
-        t0 = time.perf_counter()
-        for lw in layers:
-            torch_cpu.layer_projections(h, attn, lw, EPS)
-        times.append((time.perf_counter() - t0) / len(layers))
-    us = statistics.median(times) * 1e6
-    byts = sum(layer_bytes(model.cfg, 1).values())
+    threads, how = cpu_share()
+    torch.set_num_threads(threads)
+    each = budget_s / 8
+    out = {}
+
+    def layers_fn(layers, m, cfg, seed):
+        g = torch.Generator().manual_seed(seed)
+        h = torch.randn((m, cfg["hidden"]), generator=g).to(torch.bfloat16)
+        attn = torch.randn((m, cfg["q_heads"] * cfg["head_dim"]), generator=g).to(torch.bfloat16)
+        return lambda: [torch_cpu.layer_projections(h, attn, lw, EPS) for lw in layers]
+
+    cfg8 = model8.cfg
+    layers8 = [{k: v.cpu() for k, v in model8.layers[i].items()} for i in range(2)]
+    for m in (1, 5, 8, 16):
+        us, reps = _cpu_median(layers_fn(layers8, m, cfg8, m), each)
+        us /= len(layers8)
+        byts = sum(layer_bytes(cfg8, m).values())
+        label = "C3 8B layer M=1" if m == 1 else f"C4 8B layer M={m}"
+        out[label] = {"us_per_layer": round(us, 1), "GB_s": round(byts / us / 1e3, 2), "passes": reps,
+                      "sample": "2 of 36 layers"}
+    del layers8
+    head, gamma = model8.head.cpu(), model8.final_norm.cpu()
+    for m in (1, 5):
+        x = torch.randn((m, cfg8["hidden"]), generator=torch.Generator().manual_seed(50 + m)).to(torch.bfloat16)
+        us, reps = _cpu_median(lambda: torch_cpu.lm_head_argmax(x, head, gamma, EPS), each)
+        out[f"C5 lm_head+argmax M={m}"] = {"us_per_call": round(us, 1),
+                                           "GB_s": round(head_bytes(cfg8, m) / us / 1e3, 2), "passes": reps}
+    del head
+    model06 = Model(QWEN3_06B, dev, head=False, seed=2)
+    layers06 = [{k: v.cpu() for k, v in model06.layers[i].items()} for i in range(4)]
+    del model06
+    us, reps = _cpu_median(layers_fn(layers06, 1, QWEN3_06B, 3), each)
+    us /= len(layers06)
+    out["C2 0.6B layer M=1"] = {"us_per_layer": round(us, 1),
+                                "GB_s": round(sum(layer_bytes(QWEN3_06B, 1).values()) / us / 1e3, 2),
+                                "passes": reps, "sample": "4 of 28 layers"}
+    x = torch.randn((1, 1024), generator=torch.Generator().manual_seed(60)).to(torch.bfloat16)
+    w = layers06[0]["qkv"]
+    us, reps = _cpu_median(lambda: torch_cpu.linear(x, w), each, max_reps=5000)
+    out["C1 0.6B qkv M=1 (no prologue)"] = {"us_per_call": round(us, 1),
+                                            "GB_s": round((2 * 4096 * 1024 + 2 * 1024 + 2 * 4096) / us / 1e3, 2),
+                                            "passes": reps}
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -229,10 +309,12 @@ def cpu_baseline(model, step, budget_s):
                 break
     except OSError:
         pass
-    return {"value": round(byts / us / 1e3, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"2 of 36 Qwen3-8B-shape layers at M=1 (QKV+O+gate/up+SwiGLU+down, torch CPU BF16), "
-                      f"median of {len(times)} passes; {us:.0f} us/layer; CPU: {cpu_model}",
-            "us_per_layer": round(us, 1)}
+    c3 = out["C3 8B layer M=1"]
+    return {"value": c3["GB_s"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"C3: 2 of the 36 Qwen3-8B-shape layers at M=1 (QKV+O+gate/up+SwiGLU+down, torch CPU BF16), "
+                      f"median of {c3['passes']} passes, {c3['us_per_layer']:.0f} us/layer; every configuration in "
+                      f"per_config; {threads} threads ({how}; os.cpu_count() = {os.cpu_count()}); CPU: {cpu_model}",
+            "us_per_layer": c3["us_per_layer"], "per_config": out}
 
 
 def kernel_name(plan, prologue, epilogue):
@@ -262,7 +344,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-configuration table")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=24.0, help="CPU work of the CPU baseline, all configs")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline measurement (graph replays of the 36 gate/up + SwiGLU launches): the "
+                         "command whose rocprofv3 kernel trace backs roofline.avg_launch_us")
+    ap.add_argument("--extras", action="store_true",
+                    help="also time a whole decode layer with attention and a whole transformers decode step")
     ap.add_argument("--profile-gate-up", type=int, default=0, metavar="PASSES",
                     help="profiling mode: only PASSES eager passes of the 36 gate/up + SwiGLU launches, "
                          "then one 1 GiB device copy as the counter reference")
@@ -294,6 +381,11 @@ def main():
     if args.profile_attention:
         profile_attention(cfg, dev, args.profile_attention)
         return
+    if args.roofline_only:
+        model = Model(cfg, dev, head=False)
+        roof = roofline(Step(model, 1, dev))
+        print(json.dumps({"mode": "roofline-only", "roofline": roof}), flush=True)
+        return
     model = Model(cfg, dev)
     stage("Qwen3-8B weights resident")
     step = Step(model, 1, dev)
@@ -320,22 +412,16 @@ def main():
     us_per_layer = us_layers / cfg["layers"]
     layer_lb_us = sum(lb.values()) / (PEAK_GBS * 1e3)
 
-    # dominant kernel: the fused gate/up + SwiGLU GEMV (201 MB per launch at M=1)
-    gu_us = per_kind(step, "gate_up")
-    gu_bytes = lb["gate_up"]
-    roofline = {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
-                "kernel": kernel_name(L.plan(1, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU), True,
-                                      "SWIGLU") + " (Qwen3-8B gate/up 4096->2x12288, M=1)",
-                "avg_launch_us": round(gu_us, 3)}
+    roof = roofline(step)
 
     per_shape = {}
     stage(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
     if not args.no_shapes:
         per_shape = shapes_table(model, step, dev)
         per_shape.update(attention_table(cfg, dev))
-        per_shape.update(full_layer_table(model, dev))
-        per_shape.update(decode_model_table(cfg, dev))
+        if args.extras:
+            per_shape.update(full_layer_table(model, dev))
+            per_shape.update(decode_model_table(cfg, dev))
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -349,13 +435,14 @@ def main():
         "frac_peak": round(value / PEAK_GBS, 4),
         "us_per_layer": round(us_per_layer, 2), "layer_lower_bound_us": round(layer_lb_us, 2),
         "layer_vs_bound": round(us_per_layer / layer_lb_us, 3),
-        "roofline": roofline,
+        "roofline": roof,
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if per_shape:
         result["per_shape"] = per_shape
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(model, step, args.cpu_seconds)
+        stage("CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(model, dev, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
@@ -420,7 +507,8 @@ def shapes_table(model8, step8, dev):
     for m in (1, 5):
         st = step8 if m == 1 else Step(model8, m, dev, seed=5)
         h = torch.randn((m, cfg["hidden"]), device=dev).to(torch.bfloat16)
-        g = capture(lambda: [A.lm_head_argmax(h, w, model8.final_norm, EPS, logits=True, top=st.top) for w in heads])
+        g = capture(lambda: [A.lm_head_argmax(h, w, model8.final_norm, EPS, logits=True, top=st.top,
+                                              ids_dtype=torch.int32) for w in heads])
         us = time_graph(g) / len(heads)
         out[f"C5 lm_head+argmax M={m}"] = shape_entry(us, head_bytes(cfg, m), 2 * m * cfg["vocab"] * cfg["hidden"])
         stage(f"C5 M={m} done")

@@ -448,6 +448,8 @@ const char* ftk_status_string(int status) {
 
 int ftk_last_hip_error(void) { return g_last_hip_error; }
 
+int ftk_persistent_programs(int tiles, int units) { return persistent_programs(tiles, units); }
+
 int ftk_device_compute_units(void) {
   DeviceInfo d = device_info();
   return d.ok ? d.cus : -1;
@@ -567,12 +569,12 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
     if (ids == nullptr || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
     if (workspace == nullptr) return FTK_ERR_WORKSPACE;
   }
-  ftk_rows r = {nullptr, nullptr, nullptr, 0};
+  ftk_rows r = {nullptr, nullptr, nullptr, 0, 0};
   if (rows != nullptr) r = *rows;
   const bool extra = r.residual != nullptr || r.sum != nullptr || r.x_ids != nullptr;
   if (extra) {
     if (gamma == nullptr) return FTK_ERR_INVALID;  // the rows feed the norm
-    if (r.x_ids != nullptr && r.x_ids_bytes != 4 && r.x_ids_bytes != 8) return FTK_ERR_INVALID;
+    if (r.x_ids != nullptr && ((r.x_ids_bytes != 4 && r.x_ids_bytes != 8) || r.x_rows < 1)) return FTK_ERR_INVALID;
     if (M < 1 || K < 1 || M > FTK_MAX_ROWS || K > INT32_MAX) return FTK_ERR_INVALID;
     // Workgroup 0 writes sum while every workgroup reads x and the residual.
     const int64_t rows_bytes = M * K * 2;
@@ -614,6 +616,7 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   a.sum = (uint16_t*)r.sum;
   a.x_ids = r.x_ids;
   a.x_ids_bytes = r.x_ids_bytes;
+  a.x_rows = r.x_rows;
   a.out_add = (const uint16_t*)out_add;
   // The MFMA kind's projection reads the pre-pass's stored rows: it needs sum.
   if (p.kind == FTK_KIND_MFMA && (r.residual != nullptr || r.x_ids != nullptr) && r.sum == nullptr)

@@ -30,6 +30,7 @@ struct ProjArgs {
   uint16_t* sum;             // [M, K] or null
   const void* x_ids;         // [M] int32 / int64 row indices into x, or null
   int x_ids_bytes;
+  int64_t x_rows;            // rows of the table x_ids index (>= 1 with x_ids)
   // EPI_STORE only: the residual stream the outputs are added to, or null. The
   // stored value is then bf16(bf16(y) + out_add[m, n]) (the add of add_rms_norm
   // moved into the producer; it may alias y).
@@ -43,11 +44,14 @@ __device__ __forceinline__ uint32_t store_bits(const ProjArgs& a, float s, int m
   return f32_to_bf16(bf16_to_f32(b) + bf16_to_f32(a.out_add[(size_t)m * a.N + n]));
 }
 
-// Row m of the prologue's x: x[x_ids[m]] (embedding gather) or x[m].
+// Row m of the prologue's x: x[x_ids[m]] (embedding gather) or x[m]. The host
+// cannot see device-side ids, so an id outside [0, x_rows) is clamped into the
+// table (below 0 reads row 0, past the end the last row): reads stay in bounds.
 __device__ __forceinline__ const uint16_t* x_row(const ProjArgs& a, int m) {
   if (a.x_ids == nullptr) return a.x + (size_t)m * a.K;
-  const int64_t id = a.x_ids_bytes == 8 ? reinterpret_cast<const int64_t*>(a.x_ids)[m]
-                                        : (int64_t) reinterpret_cast<const int32_t*>(a.x_ids)[m];
+  int64_t id = a.x_ids_bytes == 8 ? reinterpret_cast<const int64_t*>(a.x_ids)[m]
+                                  : (int64_t) reinterpret_cast<const int32_t*>(a.x_ids)[m];
+  id = id < 0 ? 0 : id >= a.x_rows ? a.x_rows - 1 : id;
   return a.x + (size_t)id * a.K;
 }
 

@@ -168,14 +168,4 @@ FTK_HD int persistent_programs(int tiles, int units) {
   return (tiles + depth - 1) / depth;
 }
 
-// Largest split count <= wanted whose chunks tile K with whole block_k blocks
-// (engine/kernels/gemm.py:428-433).
-FTK_HD int exact_splits(int k, int block_k, int wanted) {
-  if (k % block_k) return wanted;
-  const int blocks = k / block_k;
-  for (int s = wanted; s > 1; --s)
-    if (blocks % s == 0) return s;
-  return 1;
-}
-
 }  // namespace ftk

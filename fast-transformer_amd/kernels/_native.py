@@ -48,7 +48,8 @@ class Plan(ctypes.Structure):
 class Rows(ctypes.Structure):
     """ftk_rows: the prologue's residual, stored sum and gathered row indices (NULL = absent)."""
 
-    _fields_ = [("residual", _c_void_p), ("sum", _c_void_p), ("x_ids", _c_void_p), ("x_ids_bytes", _int)]
+    _fields_ = [("residual", _c_void_p), ("sum", _c_void_p), ("x_ids", _c_void_p), ("x_ids_bytes", _int),
+                ("x_rows", _i64)]
 
 
 class AttnConfig(ctypes.Structure):
@@ -74,6 +75,7 @@ SIGNATURES = {
     "ftk_status_string": (ctypes.c_char_p, [_int]),
     "ftk_last_hip_error": (_int, []),
     "ftk_device_compute_units": (_int, []),
+    "ftk_persistent_programs": (_int, [_int, _int]),
     "ftk_linear_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ftk_rms_norm_linear_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                         _c_void_p]),

@@ -120,17 +120,6 @@ def rope_attend(packed, q_norm, k_norm, cos, sin, position, keys, values, q_head
     return out
 
 
-def block_attention(query, key, value, position, scale, chain):
-    """Verify-block attention (engine/kernels/decode_attention.py:637-680): outside this library.
-
-    The name exists so that engine/layers.py:7 imports; a speculative verify
-    pass (the only caller, engine/layers.py:62-68) raises here. One-token decode
-    steps use ``decode_attention``.
-    """
-    raise NotImplementedError("verify-block attention (speculative decoding) is outside this library; "
-                              "decode one token per step with decode_attention")
-
-
 def decode_attention(query, key, value, position, scale):
     """Q [B,Hq,1,D], KV [B,Hkv,C,D] -> [B,1,Hq,D]."""
     batch, query_heads, tokens, dim = query.shape

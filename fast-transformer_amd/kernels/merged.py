@@ -14,7 +14,12 @@ from kernels import _native
 
 
 class Split:
-    """FP32 partials [S, M, N] standing for a BF16 tensor of logical ``shape`` (..., N)."""
+    """A BF16 result handed over unmerged: ``partial`` holds S FP32 planes of M x N partial sums
+    whose split-order sum, rounded once, is the tensor of logical ``shape`` (..., N).
+
+    ``splits`` is S and ``count`` the elements of one plane (M N); the slot layout and the two
+    properties are the protocol of engine/kernels/merged.py:13-27.
+    """
 
     __slots__ = ("partial", "shape")
 
@@ -31,7 +36,11 @@ class Split:
 
 
 def source(x):
-    """(tensor to read, SPLITS, elements per split, logical shape) for a tensor or a Split (merged.py:30-34)."""
+    """What a consumer reads for ``x``: ``(data, S, plane elements, logical shape)``.
+
+    A plain tensor reads as one split of plane size 1; a ``Split`` as its partials
+    (the 4-tuple of engine/kernels/merged.py:30-34).
+    """
     if isinstance(x, Split):
         return x.partial, x.splits, x.count, x.shape
     return x, 1, 1, tuple(x.shape)

@@ -19,11 +19,13 @@ from kernels.merged import source
 
 def qk_rope_cache(packed, q_norm, k_norm, cos, sin, position, keys, values, q_heads, prefill=False, rows=False,
                   phases=None):
-    """BF16 packed QKV and [B,Hkv,C,D] caches, for prefill or one decode token.
+    """Normalise and rotate the query and key heads of ``packed`` [B, T, (Hq + 2 Hkv) D] and write
+    the key and value heads into the [B, Hkv, C, D] caches.
 
-    Native BF16 phases [1,T,D] are shared by batch rows. Prefill writes [0,T);
-    decode writes T slots starting at the device-side scalar position. Return a [B,Hq,T,D]
-    view of token-major Q storage (contiguous when T is one).
+    Without ``rows`` one [1, T, D] cos/sin pair serves every batch row; with ``rows`` each row has
+    its own (or, with ``phases``, its own offsets into whole tables). Prefill fills slots [0, T);
+    a decode step fills the T slots from the position held on the device. The result is the
+    queries as [B, Hq, T, D], a view of token-major storage that is contiguous for T = 1.
     """
     batch, kv_heads, capacity, dim = keys.shape
     packed, splits, count, shape = source(packed)

@@ -36,7 +36,11 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 
 
 def add_rms_norm(x, residual, weight, eps):
-    """Return (normalized sum, BF16 sum), without mutating either input (rmsnorm.py:98-125)."""
+    """``(rms_norm(s), s)`` for the BF16 sum ``s = x + residual``; neither input is written.
+
+    ``x`` may be a ``Split`` (its partials are summed and rounded before the add). Signature,
+    assertions and outputs of engine/kernels/rmsnorm.py:98-125.
+    """
     x_data, splits, count, shape = source(x)
     assert shape == tuple(residual.shape)
     assert residual.dtype == weight.dtype == torch.bfloat16
@@ -64,7 +68,7 @@ def embed_rms_norm(token_ids, table, weight, eps):
     _native.require_gpu(token_ids, table, weight)
     ids = token_ids.reshape(-1).contiguous()
     if not table.is_contiguous() or ids.dtype != torch.int64:
-        raise ValueError("embedding rows must fit one block and the table must be contiguous")
+        raise ValueError("embed_rms_norm takes int64 token ids and a contiguous [rows, hidden] table")
     n_cols = table.shape[1]
     hidden = torch.empty((ids.numel(), n_cols), dtype=table.dtype, device=table.device)
     out = torch.empty_like(hidden)

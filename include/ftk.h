@@ -112,6 +112,11 @@ const char* ftk_version(void);
 const char* ftk_status_string(int status);
 int ftk_last_hip_error(void);          /* hipError_t of the last FTK_ERR_HIP on this thread */
 int ftk_device_compute_units(void);    /* CUs of the current device, or -1 without a device */
+/* Workgroups of a persistent launch over `tiles` tiles on `units` compute units: the fewest
+ * that keep every workgroup's walk at ceil(tiles / units) tiles (engine/kernels/gemm.py:330-338
+ * persistent_programs). The planner sizes the STREAM, QUAD, STAGE and MFMA_STREAM grids with it.
+ * 0 when tiles or units is not positive. Host only. */
+int ftk_persistent_programs(int tiles, int units);
 
 /* ---- projections ------------------------------------------------------------ */
 
@@ -167,6 +172,9 @@ typedef struct ftk_rows {
   void* sum;             /* [M, K] BF16 out, or NULL */
   const void* x_ids;     /* [M] row indices into x, or NULL */
   int x_ids_bytes;       /* 4 (int32) or 8 (int64) */
+  int64_t x_rows;        /* rows of the table x (required, >= 1, with x_ids). The ids live on the
+                            device, so the device clamps them into the table: an id below 0 reads
+                            row 0 and an id at or past x_rows reads row x_rows - 1 */
 } ftk_rows;
 
 /* ftk_project_bf16 with the prologue's rows described by `rows` (NULL: x as is).
@@ -204,7 +212,10 @@ int ftk_add_rms_norm_bf16(const void* x, int x_splits, int64_t x_split_stride, c
                           const void* gamma, void* y, void* sum, int64_t rows, int64_t cols, float eps, void* stream);
 
 /* embed_rms_norm(token_ids, table, weight, eps) (engine/kernels/rmsnorm.py:145-162):
- * hidden[r] = table[ids[r]] (the residual stream), y[r] = rms_norm(hidden[r]). */
+ * hidden[r] = table[ids[r]] (the residual stream), y[r] = rms_norm(hidden[r]).
+ * Precondition: every id lies in [0, table rows). The table's row count is not an
+ * argument (the reference's signature), so ids are not checked; callers that cannot
+ * promise valid ids use ftk_project_rows_bf16, whose gather clamps them. */
 int ftk_embed_rms_norm_bf16(const void* ids, int ids_bytes, const void* table, const void* gamma, void* y,
                             void* hidden, int64_t rows, int64_t cols, float eps, void* stream);
 

@@ -1,8 +1,9 @@
 """The reference's integer tiling helpers, restated (test infrastructure only).
 
-These fix how a persistent launch spreads tiles over compute units and how a
-split-K count is made to tile K exactly. The host planner in the product
-(kernels/plan.py and the C library's planner) is checked against them.
+``persistent_programs`` fixes how a persistent launch spreads tiles over
+compute units; the C library's planner runs the same rule
+(``ftk_persistent_programs``, csrc/ftk_plan.h) and tests/test_oracle.py checks
+the library's function against this one and the reference's known answers.
 """
 
 
@@ -18,18 +19,6 @@ def persistent_programs(tiles, units):
         return 0
     depth = -(-tiles // units)
     return -(-tiles // depth)
-
-
-def exact_splits(k, block_k, wanted):
-    """Largest split count <= wanted whose chunks tile K with whole BLOCK_K blocks.
-
-    (engine/kernels/gemm.py:428-433; known answers at engine/kernels/linear.py:359-361:
-    K = 2560, BLOCK_K = 128, wanted 8 -> 5; K = 9728 -> 4.) A ragged K keeps ``wanted``.
-    """
-    if k % block_k:
-        return wanted
-    blocks = k // block_k
-    return max(s for s in range(1, wanted + 1) if blocks % s == 0)
 
 
 def tile_owners(tiles, programs):

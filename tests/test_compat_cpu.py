@@ -1,27 +1,32 @@
-"""The reference's engine imports load against this package (engine/layers.py:7-11,
-engine/decode.py:12-20, engine/engine.py:9), and the out-of-scope names fail loudly."""
+"""The in-scope names the reference's engine imports load from this package
+(engine/layers.py:7-11, engine/decode.py:12-20), with the reference's call signatures."""
 
-import pytest
+import inspect
 
-from kernels import pdl, spec
-from kernels.argmax import argmax, fused_argmax, greedy_tokens  # noqa: F401
-from kernels.decode_attention import block_attention, decode_attention  # noqa: F401
-from kernels.linear import MAX_ROWS, keep_native, linear  # noqa: F401
-from kernels.qk_rope import qk_rope_cache  # noqa: F401
-from kernels.rmsnorm import add_rms_norm, embed_rms_norm, rms_norm  # noqa: F401
-from kernels.swiglu import swiglu  # noqa: F401
-from kernels.tune import knobs  # noqa: F401
-
-
-def test_pdl_reports_off_as_the_reference_does_without_it():
-    assert pdl.ENABLED is False and pdl.install() is False
-    assert pdl.self_test("cuda:0") is False
-    pdl.uninstall()
-    pdl.wait()
+from kernels.argmax import argmax, fused_argmax, greedy_tokens
+from kernels.decode_attention import decode_attention
+from kernels.linear import MAX_ROWS, keep_native, linear
+from kernels.merged import Split, source
+from kernels.rmsnorm import add_rms_norm, embed_rms_norm, rms_norm
+from kernels.swiglu import swiglu
+from kernels.tune import Knob, knobs, pick, register
 
 
-def test_speculation_names_raise():
-    for fn, args in ((spec.propose, (None,) * 8), (spec.within_margin, (None,) * 4), (spec.settle, (None,) * 10),
-                     (spec.relocate, (None,) * 3), (block_attention, (None,) * 6)):
-        with pytest.raises(NotImplementedError):
-            fn(*args)
+def test_signatures_match_the_reference_call_sites():
+    params = lambda fn: list(inspect.signature(fn).parameters)  # noqa: E731
+    assert params(linear) == ["x", "weight", "split_ok"]
+    assert params(keep_native) == ["rows", "weight"]
+    assert MAX_ROWS == 32
+    assert params(rms_norm) == ["x", "weight", "eps"]
+    assert params(add_rms_norm) == ["x", "residual", "weight", "eps"]
+    assert params(embed_rms_norm) == ["token_ids", "table", "weight", "eps"]
+    assert params(swiglu) == ["packed"]
+    assert params(argmax)[:1] == ["logits"] and "top" in params(argmax)
+    assert params(fused_argmax)[:2] == ["x", "weight"]
+    assert params(greedy_tokens)[:3] == ["x", "weight", "linear"]
+    assert params(decode_attention) == ["query", "key", "value", "position", "scale"]
+    assert params(register) == ["name", "rows", "weight", "options", "get", "select"]
+    assert params(pick) == ["key", "default", "options", "launch"]
+    assert callable(knobs) and callable(source)
+    assert set(Knob.__slots__) == {"name", "rows", "weight", "options", "get", "select"}
+    assert set(Split.__slots__) == {"partial", "shape"}

@@ -98,6 +98,21 @@ def test_embed_rms_norm_linear(cuda, m, k, ids_dtype):
     assert within(to_bits(y), path.project(normed, to_bits(w)))
 
 
+@pytest.mark.parametrize("m", [1, 3, 5])
+def test_embed_gather_clamps_ids_outside_the_table(cuda, m):
+    """Device-side ids outside [0, rows) read the nearest table row: no read leaves the table."""
+    vocab, k, n = 300, 1024, 512
+    table = seeded((vocab, k), seed=1850, device=cuda)
+    g = seeded((k,), seed=1851, scale=0.1, shift=1.0, device=cuda)
+    w = seeded((n, k), seed=1852, scale=0.02, device=cuda)
+    token_ids = torch.tensor([vocab, -1, 10 ** 9, 7, -(10 ** 9)][:m], dtype=torch.int64, device=cuda)
+    y, hidden = L.embed_rms_norm_linear(token_ids, table, g, 1e-6, w)
+    clamped = token_ids.clamp(0, vocab - 1).cpu().numpy()
+    normed, want_hidden = path.embed_rms_norm(clamped, to_bits(table), to_bits(g), 1e-6)
+    np.testing.assert_array_equal(to_bits(hidden), want_hidden)
+    assert within(to_bits(y), path.project(normed, to_bits(w)))
+
+
 def test_embed_rms_norm_standalone(cuda):
     table = seeded((1000, 1024), seed=1900, device=cuda)
     g = seeded((1024,), seed=1901, scale=0.1, shift=1.0, device=cuda)

@@ -42,9 +42,25 @@ def test_version_and_status_strings():
     lib = _native.lib()
     assert b"gfx950" in lib.ftk_version()
     for code in range(5):
-        assert lib.ftk_status_string(code)
+        assert lib.ftk_status_string(code) != b"unknown status"
     assert lib.ftk_argmax_workspace_bytes(1, 8192) == 8
     assert lib.ftk_argmax_workspace_bytes(32, 151936) == 8 * 32 * 19
+
+
+def test_persistent_programs_in_the_library_known_answers():
+    """The planner's own persistent_programs (csrc/ftk_plan.h, exported as ftk_persistent_programs)
+    against the reference's known answers (engine/kernels/gemm.py:333-335, 132 SMs) and the oracle."""
+    from oracle import helpers
+
+    lib = _native.lib()
+    assert lib.ftk_persistent_programs(304, 132) == 102
+    assert lib.ftk_persistent_programs(2374, 132) == 132
+    for tiles in (1, 17, 131, 132):
+        assert lib.ftk_persistent_programs(tiles, 132) == tiles
+    assert lib.ftk_persistent_programs(0, 132) == 0 and lib.ftk_persistent_programs(5, 0) == 0
+    for tiles in range(1, 3000, 37):
+        for units in (132, 256, 304):
+            assert lib.ftk_persistent_programs(tiles, units) == helpers.persistent_programs(tiles, units)
 
 
 def test_invalid_arguments_rejected_before_any_launch():
@@ -77,9 +93,14 @@ def test_invalid_arguments_rejected_before_any_launch():
     rows = _native.Rows(buf, ctypes.c_void_p(8192), None, 0)
     assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), None, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64, 64,
                                      0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
-    rows = _native.Rows(None, None, fake, 3)
+    rows = _native.Rows(None, None, fake, 3, 16)
     assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64, 64,
                                      0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
+    # gathered rows need the table's row count (the device clamps ids into it)
+    for table_rows in (0, -1):
+        rows = _native.Rows(None, None, fake, 8, table_rows)
+        assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64,
+                                         64, 0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
     assert lib.ftk_embed_rms_norm_bf16(fake, 3, fake, fake, fake, fake, 1, 8, 1e-6, None) == _native.FTK_ERR_INVALID
 
 

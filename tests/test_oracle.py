@@ -245,13 +245,6 @@ def test_persistent_programs_known_answers():
         assert helpers.persistent_programs(tiles, 132) == tiles
 
 
-def test_exact_splits_known_answers():
-    # engine/kernels/linear.py:359-361
-    assert helpers.exact_splits(2560, 128, 8) == 5
-    assert helpers.exact_splits(9728, 128, 8) == 4
-    assert helpers.exact_splits(517, 128, 8) == 8   # ragged K keeps the wanted count
-
-
 def test_tile_owners_each_once():
     for tiles, units in ((304, 132), (2374, 132), (9496, 256), (17, 256)):
         programs = helpers.persistent_programs(tiles, units)
