@@ -3,6 +3,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/ftk.h"
 #include "ftk_internal.h"
 
@@ -427,6 +429,36 @@ static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, i
   return FTK_OK;
 }
 
+// ---- static scratch of the entry point that allocates nothing ----------------
+// File-scope device array: every GPU the library runs on holds its own copy,
+// at its own address, until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// it passes the device address hipGetSymbolAddress returned for the current
+// device, looked up once per device and kept here.
+static __device__ __align__(256) unsigned char scratch[FTK_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_lock;
+
+// The current device's address of `scratch` (looked up on the first call on that device).
+static int static_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  if (dev < 0 || dev >= kMaxDevices) return FTK_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_scratch_lock);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e);
+    if (ptr == nullptr) return hip_status(hipErrorInvalidSymbol);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FTK_OK;
+}
+
 }  // namespace ftk
 
 using namespace ftk;
@@ -442,6 +474,7 @@ const char* ftk_status_string(int status) {
     case FTK_ERR_UNSUPPORTED: return "shape or alignment not supported by this entry point";
     case FTK_ERR_WORKSPACE: return "workspace missing or too small";
     case FTK_ERR_HIP: return "HIP launch failed";
+    case FTK_ERR_TOO_LARGE: return "the call needs more scratch than the static array holds (FTK_STATIC_SCRATCH_BYTES)";
   }
   return "unknown status";
 }
@@ -719,6 +752,26 @@ int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const v
   if (K % 8) return FTK_ERR_UNSUPPORTED;
   return ftk_project_bf16(x, gamma, eps, w, logits, M, V, K, FTK_EPI_ARGMAX, ids, ids_bytes, top, workspace,
                           workspace_bytes, nullptr, stream);
+}
+
+int ftk_lm_head_argmax_static_bf16(const void* x, const void* gamma, float eps, const void* w, void* logits,
+                                   void* ids, int ids_bytes, float* top, int64_t M, int64_t V, int64_t K,
+                                   void* stream) {
+  if (K % 8) return FTK_ERR_UNSUPPORTED;
+  if (x == nullptr || w == nullptr || ids == nullptr || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
+  DeviceInfo d = device_info();
+  if (!d.ok) return hip_status(hipErrorNoDevice);
+  ftk_plan p;
+  const int st = plan(M, V, K, FTK_EPI_ARGMAX | (gamma != nullptr ? FTK_PLAN_PROLOGUE : 0), d.cus, nullptr, &p);
+  if (st != FTK_OK) return st;
+  // Every key slot the finalize pass reads is written earlier in the same call,
+  // so the array needs no clearing between calls.
+  if (call_workspace(p, FTK_EPI_ARGMAX, gamma != nullptr) > FTK_STATIC_SCRATCH_BYTES) return FTK_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const int got = static_scratch(&ws);
+  if (got != FTK_OK) return got;
+  return project_impl(x, nullptr, gamma, eps, w, logits, M, V, K, FTK_EPI_ARGMAX, ids, ids_bytes, top, ws,
+                      FTK_STATIC_SCRATCH_BYTES, nullptr, nullptr, stream);
 }
 
 int ftk_rms_norm_bf16(const void* x, int64_t row_stride, const void* gamma, void* y, int64_t rows, int64_t cols,

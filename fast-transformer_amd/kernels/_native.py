@@ -14,7 +14,8 @@ import torch
 
 LIB_PATH = Path(__file__).with_name("libftk.so")
 
-FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP = range(5)
+FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP, FTK_ERR_TOO_LARGE = range(6)
+STATIC_SCRATCH_BYTES = 1 << 20  # FTK_STATIC_SCRATCH_BYTES
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
 PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
 KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE = range(8)
@@ -83,6 +84,8 @@ SIGNATURES = {
                                        _c_void_p]),
     "ftk_lm_head_argmax_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _c_void_p, _int,
                                        _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p]),
+    "ftk_lm_head_argmax_static_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _c_void_p, _int,
+                                              _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ftk_project_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64, _int,
                                 _c_void_p, _int, _c_void_p, _c_void_p, _i64, ctypes.POINTER(Config), _c_void_p]),
     "ftk_project_add_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,

@@ -41,8 +41,13 @@ typedef enum ftk_status {
   FTK_ERR_INVALID = 1,      /* null pointer, non-positive size, M > FTK_MAX_ROWS, bad flag */
   FTK_ERR_UNSUPPORTED = 2,  /* shape/alignment this fused entry point does not take (K % 8, 16-byte alignment) */
   FTK_ERR_WORKSPACE = 3,    /* workspace missing or smaller than *_workspace_bytes() */
-  FTK_ERR_HIP = 4           /* the HIP launch failed; see ftk_last_hip_error() */
+  FTK_ERR_HIP = 4,          /* the HIP launch failed; see ftk_last_hip_error() */
+  FTK_ERR_TOO_LARGE = 5     /* the call needs more scratch than FTK_STATIC_SCRATCH_BYTES
+                               (ftk_lm_head_argmax_static_bf16) */
 } ftk_status;
+
+/* Bytes of the static device scratch array of ftk_lm_head_argmax_static_bf16 (one per GPU). */
+#define FTK_STATIC_SCRATCH_BYTES (1 << 20)
 
 typedef enum ftk_epilogue {
   FTK_EPI_STORE = 0,   /* y[m, n] = bf16(sum) */
@@ -147,6 +152,19 @@ int ftk_gate_up_swiglu_bf16(const void* x, const void* gamma, float eps, const v
 int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const void* w, void* logits, void* ids,
                             int ids_bytes, float* top, int64_t M, int64_t V, int64_t K, void* workspace,
                             int64_t workspace_bytes, void* stream);
+
+/* ftk_lm_head_argmax_bf16 for callers that cannot allocate device memory: code under
+ * graph capture that may not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation. No counterpart in the reference. It takes no workspace and allocates nothing:
+ * the per-workgroup argmax keys live in a static device array of FTK_STATIC_SCRATCH_BYTES
+ * (1 MiB) that every GPU the library runs on holds until the process ends. Results are those of
+ * ftk_lm_head_argmax_bf16 bit for bit (same kernels). A call that needs more keys than the array
+ * holds (e.g. 32 rows of a 151936-entry vocabulary) returns FTK_ERR_TOO_LARGE and launches nothing.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and give wrong ids; keep them in one stream. */
+int ftk_lm_head_argmax_static_bf16(const void* x, const void* gamma, float eps, const void* w, void* logits,
+                                   void* ids, int ids_bytes, float* top, int64_t M, int64_t V, int64_t K,
+                                   void* stream);
 
 /* Workspace bytes ftk_project_bf16 needs for this shape on the current device:
  * per-workgroup argmax keys (FTK_EPI_ARGMAX) and the RMSNorm row scales of the

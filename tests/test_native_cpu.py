@@ -41,7 +41,7 @@ def test_binding_signatures_cover_header():
 def test_version_and_status_strings():
     lib = _native.lib()
     assert b"gfx950" in lib.ftk_version()
-    for code in range(5):
+    for code in range(6):
         assert lib.ftk_status_string(code) != b"unknown status"
     assert lib.ftk_argmax_workspace_bytes(1, 8192) == 8
     assert lib.ftk_argmax_workspace_bytes(32, 151936) == 8 * 32 * 19
