@@ -534,12 +534,16 @@ def shapes_table(model8, step8, dev):
     us = time_graph(g, reps=5) / cfg["layers"]
     out["C3 8B layer M=1, residual add in the O / down epilogues"] = shape_entry(
         us, sum(lb.values()) + 4 * 2 * cfg["hidden"])
+    del g
+    out.update(chain_entry("C3 8B layer M=1, all 36 layers in one chain launch", step8, sum(lb.values())))
     # C1 / C2: Qwen3-0.6B shapes
     model06 = Model(QWEN3_06B, dev, head=False, seed=2)
     st06 = Step(model06, 1, dev, seed=3)
     g = capture(st06.layers)
     us = time_graph(g, reps=10) / QWEN3_06B["layers"]
     out["C2 0.6B layer M=1"] = shape_entry(us, sum(layer_bytes(QWEN3_06B, 1).values()))
+    out.update(chain_entry("C2 0.6B layer M=1, all 28 layers in one chain launch", st06,
+                           sum(layer_bytes(QWEN3_06B, 1).values())))
     x = torch.randn((1, 1024), device=dev).to(torch.bfloat16)
     copies = [torch.randn((4096, 1024), device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(64)]
     ys = [torch.empty((1, 4096), device=dev, dtype=torch.bfloat16) for _ in range(64)]
@@ -548,6 +552,26 @@ def shapes_table(model8, step8, dev):
     out["C1 0.6B qkv M=1 (no prologue)"] = shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096)
     del model06, copies
     return out
+
+
+def chain_entry(label, step, layer_bytes_):
+    """The same M=1 projection set as ``Step.layers`` run as one projection chain (kernels/chain.py): one
+    cooperative launch for every layer, O fenced behind its layer's QKV as attention would be. µs per
+    layer over graph replays, plus each stage's median share from the kernel's own clock stamps."""
+    from kernels import chain as CH
+
+    n = len(step.model.layers)
+    chain, _ = CH.decode_layers(step.model.layers, step.h, step.attn, EPS, outputs="qkv")
+    chain.prepare()
+    chain.launch()
+    chain.status()
+    g = capture(chain.launch, warm=0)
+    us = time_graph(g, reps=10) / n
+    chain.status()
+    st = chain.stage_us()
+    stages = {name: round(statistics.median(st[k::4]), 2) for k, name in enumerate(("qkv", "o", "gate_up", "down"))}
+    del g, chain
+    return {label: {**shape_entry(us, layer_bytes_), "stage_us": stages}}
 
 
 #: Decode attention next to the projections (Qwen3-8B heads: 32 query, 8 KV, D = 128):

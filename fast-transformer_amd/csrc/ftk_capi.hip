@@ -12,7 +12,7 @@ namespace ftk {
 
 static thread_local int g_last_hip_error = 0;
 
-static int hip_status(hipError_t e) {
+int hip_status(hipError_t e) {
   if (e == hipSuccess) return FTK_OK;
   g_last_hip_error = (int)e;
   return FTK_ERR_HIP;

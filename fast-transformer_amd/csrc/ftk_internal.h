@@ -9,6 +9,10 @@
 
 namespace ftk {
 
+// FTK_OK for hipSuccess; otherwise records e as this thread's last HIP error
+// (ftk_last_hip_error) and returns FTK_ERR_HIP.
+int hip_status(hipError_t e);
+
 // Arguments of one skinny projection launch (GEMV or MFMA kind).
 struct ProjArgs {
   const uint16_t* x;      // [M, K] BF16, row-major, 16-byte aligned
