@@ -39,6 +39,7 @@ from kernels import decode_attention as DA  # noqa: E402
 from kernels import linear as L  # noqa: E402
 from kernels import qk_rope as R  # noqa: E402
 from kernels import swiglu as S  # noqa: E402
+from kernels.tune import knobs  # noqa: E402
 
 METRIC = "M=1 bf16 GEMV HBM GB/s (% of peak) + µs/decode-layer, Qwen3-8B shapes"
 PEAK_GBS = 8000.0          # MI355X HBM3E
@@ -164,6 +165,24 @@ def capture(fn, warm=2):
     return graph
 
 
+def tuned_graph(fn, rows, seconds, label):
+    """Warm ``fn`` with selection on (each new shape is timed once, kernels/linear.py _choose), re-judge
+    the frozen choices of batch ``rows`` inside the captured step (linear.refine, engine/decode.py:556-583),
+    then capture the final graph."""
+    if not L.TUNE:
+        return capture(fn)
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+
+    def step_seconds():
+        return time_graph(capture(fn, warm=0), reps=5) * 1e-6
+
+    us = L.refine(step_seconds, rows, seconds) * 1e6
+    stage(f"{label}: {len(knobs(rows))} shapes selected and re-judged in the captured step ({us:.1f} us)")
+    return capture(fn)
+
+
 def time_graph(graph, reps=10, inner=1):
     """Median wall time of one replay, from HIP events on the replay stream (µs)."""
     graph.replay()
@@ -178,6 +197,23 @@ def time_graph(graph, reps=10, inner=1):
         end.synchronize()
         times.append(start.elapsed_time(end) * 1e3 / inner)
     return statistics.median(times)
+
+
+def selection_summary():
+    """The frozen launch choice of every shape the run selected (kernels/linear.py _CHOICES)."""
+    names = {_native.KIND_GEMV: "gemv", _native.KIND_MFMA: "mfma", _native.KIND_STREAM: "stream",
+             _native.KIND_MFMA_STREAM: "mfma_stream", _native.KIND_QUAD: "quad", _native.KIND_STAGE: "stage"}
+    out = {}
+    for key, choice in L._CHOICES.items():
+        op, rest = (key[0], key[2:]) if isinstance(key[0], str) else ("linear", key[1:])
+        label = f"{op} M={rest[0]} N={rest[1]} K={rest[2]}"
+        if choice is None:
+            out[label] = "planner default"
+        elif choice == "native":
+            out[label] = "native (hipBLASLt via F.linear)"
+        else:
+            out[label] = names.get(choice[0], str(choice[0])) + str(list(choice[1:]))
+    return {"tuned": L.TUNE, "choices": out}
 
 
 def shape_entry(us, byts, flops=None):
@@ -348,6 +384,9 @@ def main():
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline measurement (graph replays of the 36 gate/up + SwiGLU launches): the "
                          "command whose rocprofv3 kernel trace backs roofline.avg_launch_us")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="use the planner's launch defaults: skip the timed selection of each shape at warmup "
+                         "and its refinement inside the captured step")
     ap.add_argument("--extras", action="store_true",
                     help="also time a whole decode layer with attention and a whole transformers decode step")
     ap.add_argument("--profile-gate-up", type=int, default=0, metavar="PASSES",
@@ -388,8 +427,9 @@ def main():
         return
     model = Model(cfg, dev)
     stage("Qwen3-8B weights resident")
+    L.TUNE = not args.no_tune
     step = Step(model, 1, dev)
-    graph = capture(step.run)
+    graph = tuned_graph(step.run, 1, 20.0, "M=1 step")
     layer_graph = capture(step.layers)
     stage("decode step captured")
 
@@ -437,6 +477,7 @@ def main():
         "layer_vs_bound": round(us_per_layer / layer_lb_us, 3),
         "roofline": roof,
         "device": {"name": props.name, "cus": props.multi_processor_count},
+        "selection": selection_summary(),
     }
     if per_shape:
         result["per_shape"] = per_shape
@@ -516,7 +557,7 @@ def shapes_table(model8, step8, dev):
     # C4: 8B layer set at M = 5, 8, 16
     for m in (5, 8, 16):
         st = Step(model8, m, dev, seed=m)
-        g = capture(st.layers)
+        g = tuned_graph(st.layers, m, 20.0, f"C4 M={m}")
         us = time_graph(g, reps=5) / cfg["layers"]
         byts = sum(layer_bytes(cfg, m).values())
         flops = 2 * m * sum(n * k for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)))

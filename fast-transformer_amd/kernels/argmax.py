@@ -51,7 +51,9 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     _native.require_gpu(x, weight, norm_weight, top, residual)
     if residual is not None and norm_weight is None:
         raise ValueError("a residual needs the norm it feeds (norm_weight)")
-    from kernels.linear import fused_project, linear, prefer_native
+    from torch.nn import functional as F
+
+    from kernels.linear import _as_config, _choice, _fusable, fused_project, linear, prefer_native
     from kernels.rmsnorm import add_rms_norm, rms_norm
 
     shape = x.shape
@@ -63,9 +65,26 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < m):
         raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
-    status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
-        fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
-                      config=config)
+    if config is None and residual is None and _fusable(flat, weight, norm_weight):
+        # selected like a plain projection, under its own key (kernels/linear.py _choice); the
+        # agreement check compares the logits
+        def run(choice, w, inp=flat):
+            lg = torch.empty((inp.shape[0], w.shape[0]), device=inp.device, dtype=torch.bfloat16)
+            tok = torch.empty((inp.shape[0],), device=inp.device, dtype=ids_dtype)
+            st = fused_project(inp, w, _native.EPI_ARGMAX, lg, norm_weight, eps, ids=tok, config=_as_config(choice))
+            return lg if st == _native.FTK_OK else None
+
+        def native(w):
+            return argmax(F.linear(flat if norm_weight is None else rms_norm(flat, norm_weight, eps), w))
+
+        choice = _choice("argmax", flat, weight, run, native, _native.EPI_ARGMAX, norm_weight is not None)
+        status = _native.FTK_ERR_UNSUPPORTED if choice == "native" else \
+            fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, ids=ids, top=top,
+                          config=_as_config(choice))
+    else:
+        status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
+            fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
+                          config=config)
     if status != _native.FTK_OK:
         if residual is not None:
             xn = add_rms_norm(x, residual, norm_weight, eps)[0]

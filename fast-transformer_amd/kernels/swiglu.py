@@ -39,7 +39,10 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
     _native.require_gpu(x, gate_up_weight, norm_weight, residual)
     if residual is not None and norm_weight is None:
         raise ValueError("a residual needs the norm it feeds (norm_weight)")
-    from kernels.linear import fused_project, linear, prefer_native
+    from torch.nn import functional as F
+
+    from kernels.linear import _as_config, _choice, _fusable, fused_project, linear, prefer_native
+    from kernels.rmsnorm import rms_norm
 
     shape = x.shape
     flat = x.reshape(-1, shape[-1]).contiguous()
@@ -50,9 +53,23 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
     out = torch.empty((m, n // 2), device=x.device, dtype=torch.bfloat16)
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
     summed = None if residual is None else torch.empty_like(res)
-    status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
-        fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
-                      summed=summed, config=config)
+    if config is None and residual is None and _fusable(flat, gate_up_weight, norm_weight):
+        # selected like a plain projection, under its own key (kernels/linear.py _choice)
+        def run(choice, w, inp=flat):
+            y = torch.empty((inp.shape[0], w.shape[0] // 2), device=inp.device, dtype=torch.bfloat16)
+            st = fused_project(inp, w, _native.EPI_SWIGLU, y, norm_weight, eps, config=_as_config(choice))
+            return y if st == _native.FTK_OK else None
+
+        def native(w):
+            return swiglu(F.linear(flat if norm_weight is None else rms_norm(flat, norm_weight, eps), w))
+
+        choice = _choice("swiglu", flat, gate_up_weight, run, native, _native.EPI_SWIGLU, norm_weight is not None)
+        status = _native.FTK_ERR_UNSUPPORTED if choice == "native" else \
+            fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, config=_as_config(choice))
+    else:
+        status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
+            fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
+                          summed=summed, config=config)
     if status != _native.FTK_OK:
         from kernels.rmsnorm import add_rms_norm, rms_norm
         if residual is not None:
