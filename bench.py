@@ -224,8 +224,20 @@ def shape_entry(us, byts, flops=None):
     return e
 
 
-def per_kind(step, kind, warm=2):
-    """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch."""
+def planner_config(m, n, k, epilogue, prologue):
+    """The planner's default launch for a shape as an explicit config (no selection involved)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    p = L.plan(m, n, k, epilogue, cus, None, prologue)
+    gpc = -(-p.grid // cus)
+    cfg = _native.Config(p.kind, p.rows_per_wave, p.unroll, gpc, p.waves)
+    again = L.plan(m, n, k, epilogue, cus, cfg, prologue)
+    assert (again.kind, again.grid, again.rows_per_wave, again.waves) == (p.kind, p.grid, p.rows_per_wave, p.waves)
+    return cfg
+
+
+def per_kind(step, kind, warm=2, config=None):
+    """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch.
+    ``config`` pins the gate/up launch (otherwise each call takes its frozen choice)."""
     def fn():
         for lw in step.model.layers:
             if kind == "qkv":
@@ -233,7 +245,7 @@ def per_kind(step, kind, warm=2):
             elif kind == "o":
                 L.linear(step.attn, lw["o"])
             elif kind == "gate_up":
-                S.gate_up_swiglu(step.h, lw["gate_up"], lw["ln2"], EPS)
+                S.gate_up_swiglu(step.h, lw["gate_up"], lw["ln2"], EPS, config=config)
             else:
                 L.linear(step.act_in, lw["down"])
     if kind == "down":
@@ -252,7 +264,10 @@ def roofline(step):
     at M=1), timed over graph replays of its 36 launches (distinct weights). The graph is captured
     without eager launches, so a kernel trace of ``bench.py --roofline-only`` holds replays only."""
     cfg = step.model.cfg
-    gu_us = per_kind(step, "gate_up", warm=0)
+    # the planner's default launch, pinned, so that --roofline-only (whose kernel trace backs this
+    # figure) launches exactly the same kernel and grid whether or not this run selected shapes
+    pinned = planner_config(1, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU, True)
+    gu_us = per_kind(step, "gate_up", warm=0, config=pinned)
     gu_bytes = layer_bytes(cfg, 1)["gate_up"]
     return {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
