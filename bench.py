@@ -376,9 +376,13 @@ def kernel_name(plan, prologue, epilogue):
     return f"ftk::{head}, PRO={int(prologue)}, {epilogue}> grid {plan.grid}"
 
 
+_T0 = time.monotonic()
+
+
 def stage(msg):
-    """One progress line per finished stage (stderr; the JSON result stays the only stdout line)."""
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+    """One progress line per finished stage, with the seconds since start (stderr; the JSON result
+    stays the only stdout line)."""
+    print(f"[bench] {msg} [{time.monotonic() - _T0:.0f} s]", file=sys.stderr, flush=True)
 
 
 def load_traffic():

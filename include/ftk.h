@@ -22,8 +22,12 @@
  *   - Workspaces hold per-call scratch only (per-workgroup argmax keys,
  *     RMSNorm row scales): no initial contents are required and nothing carries
  *     over between calls. Calls that share a workspace must not run
- *     concurrently. No kernel waits on another workgroup: there are no
- *     device-scope fences or tickets anywhere.
+ *     concurrently. No projection, norm, attention or argmax kernel waits on
+ *     another workgroup: they use no device-scope fences or tickets. The one
+ *     exception is the projection chain (ftk_chain_*): a cooperative launch
+ *     whose workgroups wait, with bounded polls, for words other workgroups
+ *     of the same launch store; its workspace carries an epoch between
+ *     launches (set up by ftk_chain_prepare).
  */
 #ifndef FTK_H
 #define FTK_H
