@@ -184,15 +184,36 @@ static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64
   return {0, 0, 0};
 }
 
+// RING launch shape: 8 waves split K; two units in flight, three for the long K
+// (K = 12288) at up to 8 rows, where they fit the LDS.
+struct RingDefault {
+  int kw, depth;
+};
+static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
+  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  const int c = quad_segments((int)K, 8);
+  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2}, {8, 2}};
+  for (const RingDefault& d : order)
+    if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro)) return d;
+  return {0, 0};
+}
+// Where RING beats the other kinds (MI355X, Qwen3-8B shapes, 5..16 rows): every
+// projection and SwiGLU, with or without the norm prologue; lm_head + argmax is
+// level with STAGE and stays there. Not with the prologue's residual add, which
+// RING does not take (project_impl plans such calls without it).
+static bool ring_preferred(int64_t M, int epi) { return M >= 5 && epi != FTK_EPI_ARGMAX; }
+
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
 
 static int64_t argmax_keys_bytes(int grid, int64_t M) { return kWsKeys + (int64_t)grid * M * 8; }
 
 // epi may carry FTK_PLAN_PROLOGUE: plan a call with the RMSNorm prologue.
+// epi may carry FTK_PLAN_RESIDUAL: the prologue adds a residual, which the RING kind does not take.
 static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_config* cfg, ftk_plan* p) {
   const bool pro = (epi & FTK_PLAN_PROLOGUE) != 0;
-  epi &= ~FTK_PLAN_PROLOGUE;
+  const bool ring_ok = (epi & FTK_PLAN_RESIDUAL) == 0;
+  epi &= ~(FTK_PLAN_PROLOGUE | FTK_PLAN_RESIDUAL);
   memset(p, 0, sizeof(*p));
   if (M < 1 || M > FTK_MAX_ROWS || N < 1 || K < 1 || cus < 1) return FTK_ERR_INVALID;
   if (N > INT32_MAX / 2 || K > INT32_MAX / 2) return FTK_ERR_INVALID;
@@ -206,8 +227,11 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // the shape.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     const bool stage = M >= 5 && stage_default(M, epi, pro, N, K).t != 0;
+    const bool ring = ring_ok && ring_preferred(M, epi) && ring_default(M, epi, pro, N, K).kw != 0;
     if (K % 8)
       kind = FTK_KIND_GENERIC;
+    else if (ring)
+      kind = FTK_KIND_RING;
     else if (quad && quad_preferred(M, epi, pro))
       kind = FTK_KIND_QUAD;
     else if (stage)
@@ -324,6 +348,25 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // One workgroup per CU (the LDS of one fills most of a CU), each walking its
     // share of the tiles: lm_head + argmax at 5 rows no longer runs a partial
     // last round of workgroups.
+    const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
+    p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
+    return FTK_OK;
+  }
+  if (kind == FTK_KIND_RING) {
+    if (M < 2 || M > kRingMaxRows) return FTK_ERR_UNSUPPORTED;
+    const RingDefault d = ring_default(M, epi, pro, N, K);
+    const int kw = cfg && cfg->waves ? cfg->waves : (d.kw ? d.kw : 8);
+    const int depth = cfg && cfg->unroll ? cfg->unroll : (d.depth ? d.depth : 2);
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 16;
+    if (quad_segments((int)K, kw) == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
+    if (rows != 16 || !ring_supported((int)M, (int)K, kw, depth, epi, pro)) return FTK_ERR_INVALID;
+    p->rows_per_wave = rows;
+    p->unroll = depth;
+    p->waves = kw;
+    p->threads = 64 * kw;
+    p->tiles = ring_tiles(epi, (int)N);
+    // One workgroup per CU (its LDS fills the CU), each walking its share.
     const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
@@ -562,6 +605,23 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
       }
     return FTK_OK;
   }
+  if (p->kind == FTK_KIND_RING) {
+    // Workgroup b walks tiles b + i grid; unit rows 0..15 of a tile.
+    if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
+    const int per = ring_out_per_tile(epilogue);
+    for (int b = 0; b < p->grid; ++b)
+      for (int tile = b; tile < p->tiles; tile += p->grid) {
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = ring_weight_row(epilogue, tile, r, (int)N);
+          if (row > *max_row) *max_row = row;
+        }
+        for (int r = 0; r < per; ++r) {
+          const int64_t col = (int64_t)tile * per + r;
+          if (col < outputs) counts[col] += 1;
+        }
+      }
+    return FTK_OK;
+  }
   if (p->kind != FTK_KIND_GEMV && p->kind != FTK_KIND_STREAM && p->kind != FTK_KIND_QUAD) return FTK_ERR_UNSUPPORTED;
   if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
   if ((p->kind == FTK_KIND_STREAM || p->kind == FTK_KIND_QUAD) && (p->tiles + p->grid - 1) / p->grid > kStreamMaxTiles)
@@ -620,7 +680,9 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   DeviceInfo d = device_info();
   if (!d.ok) return hip_status(hipErrorNoDevice);
   ftk_plan p;
-  int st = plan(M, N, K, epilogue | (gamma != nullptr ? FTK_PLAN_PROLOGUE : 0), d.cus, cfg, &p);
+  int st = plan(M, N, K,
+                epilogue | (gamma != nullptr ? FTK_PLAN_PROLOGUE : 0) | (r.residual != nullptr ? FTK_PLAN_RESIDUAL : 0),
+                d.cus, cfg, &p);
   if (st != FTK_OK) return st;
   const int64_t need = call_workspace(p, epilogue, gamma != nullptr);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return FTK_ERR_WORKSPACE;
@@ -654,6 +716,8 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   // The MFMA kind's projection reads the pre-pass's stored rows: it needs sum.
   if (p.kind == FTK_KIND_MFMA && (r.residual != nullptr || r.x_ids != nullptr) && r.sum == nullptr)
     return FTK_ERR_UNSUPPORTED;
+  // The RING kind loads x rows as they are: no residual add in its prologue.
+  if (p.kind == FTK_KIND_RING && r.residual != nullptr) return FTK_ERR_UNSUPPORTED;
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   hipError_t e;
@@ -669,6 +733,9 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   } else if (p.kind == FTK_KIND_STAGE) {
     StageShape g = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid, p.tiles};
     e = launch_stage(a, epilogue, g, s);
+  } else if (p.kind == FTK_KIND_RING) {
+    RingShape g = {p.unroll, p.waves, p.grid, p.tiles};
+    e = launch_ring(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};
     e = launch_gemv(a, epilogue, g, s);

@@ -129,6 +129,16 @@ struct StageShape {
 bool stage_supported(int M, int t, int K, int kw, int unroll, int epi, bool pro);
 hipError_t launch_stage(const ProjArgs& a, int epi, const StageShape& shape, hipStream_t stream);
 
+// Launch shape of the RING kind (K = 128 C KW; weights and x loaded straight into LDS).
+struct RingShape {
+  int depth;     // D: units (K segments of one tile) in flight per wave
+  int kw;        // waves per workgroup, splitting K
+  int grid;      // workgroups; each walks tiles wg, wg + grid, ...
+  int tiles;
+};
+bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro);
+hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& shape, hipStream_t stream);
+
 // Launch shape of the MFMA kind.
 struct MfmaShape {
   int subtiles;  // T: 16-row MFMA subtiles per workgroup

@@ -1,0 +1,474 @@
+// M = 2..16 skinny BF16 projection, RING kind: weight and x segments land in a
+// per-wave LDS ring by direct-to-LDS loads (global_load_lds_dwordx4) and feed
+// 16x16x32 BF16 MFMAs (v_mfma_f32_16x16x32_bf16).
+//
+// Same sums, roundings and fused extras as the other kinds
+// (engine/kernels/linear.py:50-78 _skinny_gemm; RMSNorm prologue
+// engine/kernels/rmsnorm.py:21-46; SwiGLU engine/kernels/swiglu.py:13-24;
+// greedy argmax engine/kernels/argmax.py:19-48), FP32 accumulation, one rounding.
+//
+// Why: at 5..16 rows the kernels that hold x in registers spend as many L2
+// requests on x as on the weights. An MFMA B operand needs x row l % 16 in lane
+// l, so a register load of it touches 16 rows x 64 bytes per wave instruction.
+// Here x travels like the weights, 4 rows x 256 contiguous bytes per wave
+// instruction, straight into LDS, and is read back in MFMA layout. The weight
+// window lives in LDS too, so it costs no registers.
+//
+// Layout and schedule:
+//   * A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows)
+//     over all of K. A workgroup is KW waves splitting K; wave kw owns the
+//     128-wide K segments j KW + kw (j < C, K = 128 C KW). A unit is one segment
+//     of one tile: 4 KiB of weights (4 loads of 4 rows x 256 bytes) and, while
+//     the B operand is not held in registers, 4 NX rows of x (NX loads).
+//   * Lane l of load q brings row 4 q + l / 16, chunk (l % 16) ^ h(row), into
+//     slot row * 16 + l % 16 of the unit's LDS: the XOR-swizzled layout whose
+//     MFMA reads (lane l: row l % 16, chunk 4 s + l / 16) hit 16 distinct
+//     16-byte bank groups per 16 lanes.
+//   * Each wave keeps D units in flight in its own D slots; it waits for the
+//     oldest with an exact vmcnt (direct-to-LDS loads count there and return in
+//     order), reads it into registers, refills the slot, then runs the unit's
+//     arithmetic. No other wave touches those slots, so the main loop has no
+//     barrier.
+//   * x rows past M re-read row M - 1 (in bounds); rows past 4 NX are not read
+//     (their B operand is zero). Either way they feed only MFMA output columns
+//     >= M, which are never stored.
+//   * With C <= 4 the first tile's B operands (normalised, with the prologue)
+//     stay in registers and later tiles load weights only; otherwise x is
+//     loaded with every unit.
+//   * RMSNorm prologue: a pre-pass reads the x rows (or the gathered rows)
+//     row-contiguously for their sums of squares (wave w: rows w, w + KW, ...;
+//     lanes in chunk order, the DPP tree, one barrier) and workgroup 0 stores
+//     them when asked; the gain waits in LDS; each B operand chunk is
+//     normalised as it is read. The pre-pass loads go out before the first
+//     units, so the scales are ready while those units stream. The prologue's
+//     residual add is not a RING form.
+//   * Per-tile 16 x 16 partials wait in LDS; after every DMAX tiles (and after
+//     the last) a barrier lets the workgroup sum them in wave order and run the
+//     epilogue, with the next units in flight.
+#include <type_traits>
+
+#include "ftk_device.h"
+#include "ftk_internal.h"
+
+namespace ftk {
+
+namespace {
+
+typedef __attribute__((address_space(1))) const void global_void_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16 bytes per lane from `src` into LDS at dst + 16 lane (dst is wave-uniform).
+// AUX 2: non-temporal (the weights, read once per call); 0: cached (x).
+template <int AUX>
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, AUX);
+}
+
+// Wait until at most N vector memory instructions of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// LDS reads of the ring and the gain. The compiler cannot tell which ring slot
+// a direct-to-LDS load writes, so before a plain LDS read it would wait for
+// every such load in flight (vmcnt(0)), emptying the ring. These reads are
+// ordered by the explicit vmcnt waits instead; lds_ready() waits for them, and
+// ties their registers so that no use is scheduled before the wait.
+__device__ __forceinline__ u32x4_t lds_read16(const u32x4_t* p) {
+  u32x4_t v;
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const u32x4_t*)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(at) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lds_ready(u32x4_t (&v)[N]) {
+  static_assert(N == 4 || N == 8 || N == 12, "operand sets of one unit");
+  if constexpr (N == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
+  else if constexpr (N == 8)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])::"memory");
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
+                   "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])::"memory");
+}
+
+// Global loads and LDS accesses of the prologue, issued as inline assembly. The
+// compiler counts plain loads and direct-to-LDS loads in flight together as
+// possibly out of order, so before the first use of a plain load's result it
+// would wait for every load (vmcnt(0)), the first units included. These are
+// ordered by explicit waits instead: after the wait, tie() marks the registers
+// as produced there, so no use is scheduled before it.
+__device__ __forceinline__ u32x4_t asm_load16(const void* p) {
+  u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ void tie(u32x4_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void lds_write16(u32x4_t* p, u32x4_t v) {
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4_t*)p;
+  asm volatile("ds_write_b128 %0, %1" ::"v"(at), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write_f32(float* p, float v) {
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)p;
+  asm volatile("ds_write_b32 %0, %1" ::"v"(at), "v"(v) : "memory");
+}
+__device__ __forceinline__ float lds_read_f32(const float* p) {
+  float v;
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const float*)p;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(at) : "memory");
+  return v;
+}
+
+// Workgroup barrier for LDS traffic only. __syncthreads() also waits for every
+// vector memory operation (vmcnt(0)), which would empty the ring mid-walk.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+}  // namespace
+
+template <int C, int KW, int D, int NX, bool PRO, int EPI>
+__global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
+  static_assert(C % D == 0, "a tile's units must fill the ring exactly");
+  static_assert(NX == 2 || NX == 4, "x rows per unit: 8 or 16");
+  constexpr bool XREG = C <= 4;                     // B operands kept after the first tile
+  constexpr int XS = 64 * NX;                       // x slots (16 bytes) per unit
+  constexpr int SLOT = 256 + XS;                    // slots per unit
+  constexpr int DMAX = ring_max_depth(C, KW, D, NX, PRO);
+  static_assert(DMAX >= 1, "the ring leaves no LDS for the partials");
+  constexpr int GCH = PRO ? 16 * C * KW : 1;        // 16-byte chunks of the gain (K / 8)
+  __shared__ u32x4_t ring[KW][D][SLOT];
+  __shared__ f32x4_t part[DMAX][KW][64];
+  __shared__ u32x4_t gain[GCH];
+  __shared__ float red[16];
+  __shared__ unsigned long long best_lds[KW][16];
+
+  const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
+  const int li = lane & 15, g = lane >> 4;  // MFMA layout: row li, k quarter g
+  const int M = a.M, K = a.K;               // K == 128 C KW (checked by the planner)
+  const int wg = blockIdx.x, G = gridDim.x;
+  const int my_tiles = (tiles - wg + G - 1) / G;  // tiles wg, wg + G, ... (grid <= tiles)
+  const int outputs = gemv_outputs(EPI, a.N);
+
+  // ---- where this lane's loads go -------------------------------------------
+  // Load q brings unit row 4 q + lane / 16; its chunk within the segment is
+  // swizzled so that it lands in slot row * 16 + lane % 16.
+  int w_chunk[4];  // element offset of this lane's swizzled chunk in unit row 4 q + lane / 16
+  int x_off[NX];
+  const size_t seg0 = (size_t)kw * 128;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) w_chunk[q] = 8 * ((lane & 15) ^ ring_swz(4 * q + (lane >> 4)));
+  const uint16_t* xrow[NX];
+#pragma unroll
+  for (int q = 0; q < NX; ++q) {
+    const int row = 4 * q + (lane >> 4);
+    const int r = row < M ? row : M - 1;
+    xrow[q] = PRO ? x_row(a, r) : a.x + (size_t)r * K;
+    x_off[q] = 8 * ((lane & 15) ^ ring_swz(row));
+  }
+  auto issue = [&](int t, int j, int slot, bool with_x) {
+    u32x4_t* dst = ring[kw][slot];
+    const size_t k0 = seg0 + (size_t)j * KW * 128;
+    if (with_x) {
+#pragma unroll
+      for (int q = 0; q < NX; ++q) dma16<0>(xrow[q] + k0 + x_off[q], dst + 256 + 64 * q);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = ring_weight_row(EPI, t, 4 * q + (lane >> 4), a.N);
+      dma16<2>(a.w + (size_t)row * K + k0 + w_chunk[q], dst + 64 * q);
+    }
+  };
+
+  // ---- RMSNorm prologue, part 1: the gain and the x rows (row-contiguous), issued
+  // before the first units so that they return first (loads complete in order) --
+  constexpr int GPT = PRO ? (GCH + 64 * KW - 1) / (64 * KW) : 1;
+  constexpr int RPW = (16 + KW - 1) / KW;  // rows per wave at most
+  constexpr int CPL = C * KW / 4;          // chunks per lane per row: K / 512
+  u32x4_t gl[GPT];
+  u32x4_t xv[PRO ? RPW : 1][PRO ? CPL : 1];
+  if constexpr (PRO) {
+    static_assert(CPL * 512 == 128 * C * KW, "K must be a multiple of 512 for the prologue");
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int c = tid + i * 64 * KW;
+      gl[i] = asm_load16(a.gamma + (size_t)(c < GCH ? c : 0) * 8);
+    }
+    // Rows kw + i KW; waves past the last row load nothing (the wait below counts
+    // only the units issued after these loads).
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int m = kw + i * KW;
+      if (m < M) {  // wave-uniform
+        const uint16_t* xr = x_row(a, m);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) xv[i][c] = asm_load16(xr + (size_t)(lane + 64 * c) * 8);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) xv[i][c] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+
+  // ---- the first D units (all of the first tile: D <= C) ----------------------
+  asm volatile("" ::: "memory");  // keep the prologue's loads ahead of the units (the count below)
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(wg, d, d, true);
+
+  // ---- RMSNorm prologue, part 2: row scales while the first units stream -------
+  float scale = 0.f;
+  if constexpr (PRO) {
+    wait_vm<D * (4 + NX)>();  // the gain and x rows are in; the D units may still be in flight
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) tie(gl[i]);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) tie(xv[i][c]);
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int c = tid + i * 64 * KW;
+      if (c < GCH) lds_write16(gain + c, gl[i]);
+    }
+    // The rows the norm reads (the gathered rows) go out once, from workgroup 0.
+    if (a.sum != nullptr && wg == 0) {
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        const int m = kw + i * KW;
+        if (m < M) {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) store16(a.sum + (size_t)m * K + (size_t)(lane + 64 * c) * 8, xv[i][c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) ss = sum_squares8(xv[i][c], ss);
+      const float total = wave_sum(ss);
+      const int m = kw + i * KW;
+      if (lane == 0 && m < 16) lds_write_f32(red + m, total);
+    }
+    lds_barrier();
+    scale = li < M ? 1.0f / sqrtf(lds_read_f32(red + li) / (float)K + a.eps) : 0.f;
+  }
+
+  // ---- epilogue of parked tiles: thread e takes (tile i, lane position ln);
+  // D[4 gg + r][ll] of a tile is unit row 4 gg + r, x row ll ------------------
+  unsigned long long best = 0ull;
+  auto flush = [&](int n, int done) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      // Gate rows 4 h + r sit at gg = h, the matching up rows at gg = 2 + h.
+      const int entries = n * 32;
+      for (int e = tid; e < entries; e += 64 * KW) {
+        const int ll = e & 15, h = (e >> 4) & 1, i = e >> 5;
+        if (ll >= M) continue;
+        const int tl = wg + (done + i) * G;
+        f32x4_t s = part[i][0][h * 16 + ll];
+        f32x4_t u = part[i][0][(2 + h) * 16 + ll];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) {
+          s += part[i][w][h * 16 + ll];
+          u += part[i][w][(2 + h) * 16 + ll];
+        }
+        const int c0 = tl * 8 + 4 * h;
+        uint16_t* yr = a.y + (size_t)ll * outputs;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (c0 + r < outputs) yr[c0 + r] = (uint16_t)swiglu_bf16(s[r], u[r]);
+      }
+    } else {
+      const int entries = n * 64;
+      for (int e = tid; e < entries; e += 64 * KW) {
+        const int ln = e & 63, i = e >> 6;
+        const int ll = ln & 15, gg = ln >> 4;
+        if (ll >= M) continue;
+        const int tl = wg + (done + i) * G;
+        f32x4_t s = part[i][0][ln];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) s += part[i][w][ln];
+        const int n0 = tl * 16 + 4 * gg;
+        uint32_t bits[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (EPI == EPI_STORE)
+            bits[r] = n0 + r < a.N ? store_bits(a, s[r], ll, n0 + r) : 0u;
+          else
+            bits[r] = f32_to_bf16(s[r]);
+        }
+        if (a.y != nullptr) {
+          uint16_t* yr = a.y + (size_t)ll * a.N;
+          if (n0 + 3 < a.N && (a.N & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0) {
+            *reinterpret_cast<u32x2_t*>(yr + n0) = u32x2_t{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n0 + r < a.N) yr[n0 + r] = (uint16_t)bits[r];
+          }
+        }
+        if constexpr (EPI == EPI_ARGMAX) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n0 + r < a.N) best = key_max(best, argmax_key(bf16_to_f32(bits[r]), (uint32_t)(n0 + r)));
+        }
+      }
+    }
+  };
+
+  // ---- the walk --------------------------------------------------------------
+  const int rd = li * 16, hs = ring_swz(li);
+  const bool x_real = li < 4 * NX;
+  u32x4_t xr[XREG ? C : 1][4];
+  int count = 0, done = 0;
+  for (int i = 0; i < my_tiles; ++i) {
+    const int tile = wg + i * G;
+    const bool first = i == 0;
+    const bool more = i + 1 < my_tiles;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    static_for<0, C>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      constexpr int slot = j % D;
+      // Units issued after this one: the rest of the ring in this tile, then
+      // (with more tiles) the first units of the next one.
+      constexpr int n_same = (D - 1) < (C - 1 - j) ? (D - 1) : (C - 1 - j);
+      constexpr int n_next = (D - 1) - n_same;
+      constexpr int later_x = XREG ? 0 : NX;  // x loads of a unit of a later tile
+      constexpr int w_first_more = n_same * (4 + NX) + n_next * (4 + later_x);
+      constexpr int w_first_last = n_same * (4 + NX);
+      constexpr int w_later_more = n_same * (4 + later_x) + n_next * (4 + later_x);
+      constexpr int w_later_last = n_same * (4 + later_x);
+      if (first) {
+        if (more) wait_vm<w_first_more>(); else wait_vm<w_first_last>();
+      } else {
+        if (more) wait_vm<w_later_more>(); else wait_vm<w_later_last>();
+      }
+      const u32x4_t* u = ring[kw][slot];
+      const size_t kseg = seg0 + (size_t)j * KW * 128;
+      // One unit's operands: weights [0, 4), x [4, 8), gain [8, 12).
+      constexpr int NOPS = PRO ? 12 : 8;
+      u32x4_t op[NOPS];
+      const bool fresh = !XREG || first;  // B operands come from this unit's x
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int at = rd + ((4 * s + g) ^ hs);
+        op[s] = lds_read16(u + at);
+        if (fresh) {
+          op[4 + s] = lds_read16(u + 256 + (x_real ? at : 0));
+          if constexpr (PRO) op[8 + s] = lds_read16(gain + ((kseg + 32 * s + 8 * g) >> 3));
+        }
+      }
+      lds_ready(op);
+      // The slot's contents are in registers: refill it before the arithmetic,
+      // so the next load is not held back by the normalisation and the MFMAs.
+      if constexpr (j + D < C) {
+        issue(tile, j + D, slot, first || !XREG);
+      } else {
+        if (more) issue(tile + G, j + D - C, slot, !XREG);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4_t b;
+        if (fresh) {
+          b = x_real ? op[4 + s] : u32x4_t{0u, 0u, 0u, 0u};
+          if constexpr (PRO) b = norm8(b, op[8 + s], scale);
+          if constexpr (XREG) xr[j][s] = b;
+        } else {
+          b = xr[XREG ? j : 0][s];
+        }
+        acc = mfma16x16x32(op[s], b, acc);
+      }
+    });
+    part[count][kw][lane] = acc;
+    ++count;
+    if (count == DMAX || !more) {  // workgroup-uniform: every wave walks the same tiles
+      lds_barrier();
+      flush(count, done);
+      done += count;
+      count = 0;
+      if (!more) break;
+      lds_barrier();  // the next tiles park in the same slots
+    }
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    // Lanes ll, ll + 16, ll + 32, ll + 48 of every wave hold keys of x row ll.
+    best = key_max(best, __shfl_xor(best, 16));
+    best = key_max(best, __shfl_xor(best, 32));
+    if (g == 0) best_lds[kw][li] = best;
+    __syncthreads();
+    if (tid < M) {
+      unsigned long long k = best_lds[0][tid];
+      for (int w = 1; w < KW; ++w) k = key_max(k, best_lds[w][tid]);
+      a.keys[(size_t)wg * M + tid] = k;
+    }
+  }
+}
+
+// ---- dispatch -------------------------------------------------------------------
+
+typedef void (*RingKernel)(ProjArgs, int);
+
+// Instantiated (C, KW, D, NX): K = 4096 (C = 4 at 8 waves, with or without the
+// prologue, every epilogue) with two units in flight; K = 12288 (C = 12, no
+// prologue, STORE) with two or three (three only for 8 x rows: 16 would not fit
+// the LDS). NX = 2 serves 2..8 rows, NX = 4 9..16.
+#define FTK_RING_SHAPE(C_, KW_, D_, NX_, PRO, EPI) \
+  if (c == C_ && kw == KW_ && d == D_ && nx == NX_) return ring_kernel<C_, KW_, D_, NX_, PRO, EPI>;
+
+template <bool PRO, int EPI>
+static RingKernel pick_ring_shape(int c, int kw, int d, int nx) {
+  FTK_RING_SHAPE(4, 8, 2, 2, PRO, EPI)
+  FTK_RING_SHAPE(4, 8, 2, 4, PRO, EPI)
+  if constexpr (!PRO && EPI == EPI_STORE) {
+    FTK_RING_SHAPE(12, 8, 2, 2, PRO, EPI)
+    FTK_RING_SHAPE(12, 8, 3, 2, PRO, EPI)
+    FTK_RING_SHAPE(12, 8, 2, 4, PRO, EPI)
+  }
+  return nullptr;
+}
+#undef FTK_RING_SHAPE
+
+static RingKernel pick_ring(int c, int kw, int d, int nx, bool pro, int epi) {
+  switch (epi) {
+    case EPI_STORE: return pro ? pick_ring_shape<true, EPI_STORE>(c, kw, d, nx)
+                               : pick_ring_shape<false, EPI_STORE>(c, kw, d, nx);
+    case EPI_SWIGLU: return pro ? pick_ring_shape<true, EPI_SWIGLU>(c, kw, d, nx)
+                                : pick_ring_shape<false, EPI_SWIGLU>(c, kw, d, nx);
+    case EPI_ARGMAX: return pro ? pick_ring_shape<true, EPI_ARGMAX>(c, kw, d, nx)
+                                : pick_ring_shape<false, EPI_ARGMAX>(c, kw, d, nx);
+  }
+  return nullptr;
+}
+
+bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro) {
+  const int c = quad_segments(K, kw);
+  return M >= 2 && M <= kRingMaxRows && c > 0 && pick_ring(c, kw, depth, ring_x_loads(M), pro, epi) != nullptr;
+}
+
+hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& sh, hipStream_t stream) {
+  const int c = quad_segments(a.K, sh.kw);
+  RingKernel k = c > 0 ? pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), a.gamma != nullptr, epi) : nullptr;
+  if (k == nullptr || a.M < 2 || a.M > kRingMaxRows) return hipErrorInvalidValue;
+  if (sh.grid < 1 || sh.grid > sh.tiles) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(sh.grid), dim3(64 * sh.kw), 0, stream, a, sh.tiles);
+  return hipGetLastError();
+}
+
+}  // namespace ftk

@@ -18,7 +18,8 @@ FTK_OK, FTK_ERR_INVALID, FTK_ERR_UNSUPPORTED, FTK_ERR_WORKSPACE, FTK_ERR_HIP, FT
 STATIC_SCRATCH_BYTES = 1 << 20  # FTK_STATIC_SCRATCH_BYTES
 EPI_STORE, EPI_SWIGLU, EPI_ARGMAX = range(3)
 PLAN_PROLOGUE = 0x100  # FTK_PLAN_PROLOGUE
-KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE = range(8)
+PLAN_RESIDUAL = 0x200  # FTK_PLAN_RESIDUAL
+KIND_AUTO, KIND_GEMV, KIND_MFMA, KIND_GENERIC, KIND_STREAM, KIND_MFMA_STREAM, KIND_QUAD, KIND_STAGE, KIND_RING = range(9)
 ATTN_AUTO, ATTN_ROWS, ATTN_QUAD = range(3)
 ROPE_PREFILL, ROPE_ROWS, ROPE_TABLE = 0x1, 0x2, 0x4
 MAX_ROWS = 32

@@ -255,6 +255,10 @@ def _candidates(m, n, k, epilogue=_native.EPI_STORE, prologue=False):
             for kw in (4, 8):
                 for gpc in (1, 32):
                     configs.append((_native.KIND_QUAD, rows, 0, gpc, kw))
+    if 2 <= m <= 16:
+        for depth in (2, 3):
+            for gpc in (1, 2):
+                configs.append((_native.KIND_RING, 16, depth, gpc, 8))
     if m >= 5:
         for rows in (16, 32):
             for unroll in (2, 3, 4):
@@ -451,9 +455,10 @@ def linear(x, weight, split_ok=False):
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
 
-def plan(m, n, k, epilogue=_native.EPI_STORE, compute_units=256, config=None, prologue=False):
-    """The launch the C planner makes for a shape (host only; no device needed)."""
+def plan(m, n, k, epilogue=_native.EPI_STORE, compute_units=256, config=None, prologue=False, residual=False):
+    """The launch the C planner makes for a shape (host only; no device needed). ``residual``: the
+    prologue adds a residual (add_rms_norm_linear and the residual forms of the fused calls)."""
     p = _native.Plan()
-    flags = epilogue | (_native.PLAN_PROLOGUE if prologue else 0)
+    flags = epilogue | (_native.PLAN_PROLOGUE if prologue else 0) | (_native.PLAN_RESIDUAL if residual else 0)
     _native.call("ftk_plan_project", m, n, k, flags, compute_units, config, p)
     return p

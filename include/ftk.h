@@ -63,6 +63,9 @@ typedef enum ftk_epilogue {
  * plan a call that has the RMSNorm prologue (gamma != NULL). Some launch shapes
  * exist only without it, so the plan (and the workspace size) can differ. */
 #define FTK_PLAN_PROLOGUE 0x100
+/* OR-ed in as well: the call's prologue adds a residual (ftk_rows.residual). The RING kind
+ * does not take that add, so such a call is planned without it. */
+#define FTK_PLAN_RESIDUAL 0x200
 
 typedef enum ftk_kind {
   FTK_KIND_AUTO = 0,
@@ -74,8 +77,11 @@ typedef enum ftk_kind {
   FTK_KIND_MFMA_STREAM = 5, /* M <= 16, K = 32 S KW: the STREAM schedule on 16x16x32 MFMA tiles */
   FTK_KIND_QUAD = 6,        /* M <= 16, K = 128 C KW: the STREAM schedule on 16-block 4x4x4 MFMAs,
                                weights loaded as 4 rows x 256 contiguous bytes per wave load */
-  FTK_KIND_STAGE = 7        /* M <= 16, K = 128 C KW: QUAD's weight loads staged through LDS into
+  FTK_KIND_STAGE = 7,       /* M <= 16, K = 128 C KW: QUAD's weight loads staged through LDS into
                                16x16x32 MFMA tiles */
+  FTK_KIND_RING = 8         /* M = 2..16, K = 128 C KW: weight and x segments loaded straight into a
+                               per-wave LDS ring (global_load_lds_dwordx4), 16x16x32 MFMA tiles;
+                               no residual-add prologue */
 } ftk_kind;
 
 /* Launch choice for one projection (the reference's per-shape config tuple,
@@ -86,16 +92,17 @@ typedef struct ftk_config {
   int rows_per_wave;   /* GEMV, STREAM: weight rows per row group per tile (1..8);
                           MFMA: rows per workgroup (16, 32, 64); MFMA_STREAM, STAGE: rows per tile
                           (16, 32); QUAD: weight rows per row group per tile (4, 8, 16, 24; SwiGLU
-                          8, 16, 24) */
+                          8, 16, 24); RING: 16 (SwiGLU: 8 gate + 8 up rows) */
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
                           MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4);
                           STREAM, QUAD: unused (K fixes the chunks per lane);
                           MFMA_STREAM: K steps of weight loads in flight per wave (2, 4, 8);
-                          STAGE: 128-wide K segments of weight loads in flight per wave (2..6) */
-  int groups_per_cu;   /* GEMV, STREAM, MFMA_STREAM, QUAD, STAGE: grid cap = groups_per_cu * CUs (grid-stride
+                          STAGE: 128-wide K segments of weight loads in flight per wave (2..6);
+                          RING: units (K segments of a tile) in flight per wave (2; 3 at K = 12288) */
+  int groups_per_cu;   /* GEMV, STREAM, MFMA_STREAM, QUAD, STAGE, RING: grid cap = groups_per_cu * CUs (grid-stride
                           beyond; the STREAM kinds raise the grid so no workgroup walks more tiles
                           than its LDS holds); MFMA: unused */
-  int waves;           /* MFMA, MFMA_STREAM, STAGE: waves per workgroup splitting K (4, 8, 16);
+  int waves;           /* MFMA, MFMA_STREAM, STAGE, RING: waves per workgroup splitting K (4, 8, 16);
                           GEMV, STREAM: waves per row group splitting K (1, 2, 4, 8; a workgroup is
                           4 waves, or 8 when 8 split K);
                           QUAD: waves per row group splitting K (4, 8, 16; the workgroup is

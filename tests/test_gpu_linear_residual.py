@@ -39,6 +39,7 @@ CONFIGS = [
     (_cfg(_native.KIND_STREAM, 4, 0, 0, 4), (5, 8)),
     (_cfg(_native.KIND_QUAD, 8, 0, 0, 8), (2, 5, 8, 16)),
     (_cfg(_native.KIND_STAGE, 16, 2, 0, 8), (5, 9, 16)),
+    (_cfg(_native.KIND_RING, 16, 2, 0, 8), (2, 5, 9, 16)),
     (_cfg(_native.KIND_MFMA_STREAM, 16, 4, 0, 8), (5, 16)),
     (_cfg(_native.KIND_GEMV, 2, 2, 0, 2), (1, 4)),
     (_cfg(_native.KIND_MFMA, 16, 4, 0, 4), (1, 16, 32)),

@@ -55,7 +55,7 @@ CASES = [
 @pytest.mark.parametrize("m,n,k,kind", CASES)
 def test_add_rms_norm_linear(cuda, m, n, k, kind):
     x, r, w, g = _inputs(m, n, k, seed=1500 + m + k, device=cuda)
-    assert L.plan(m, n, k, prologue=True).kind == kind
+    assert L.plan(m, n, k, prologue=True, residual=True).kind == kind
     x0, r0 = x.clone(), r.clone()
     y, summed = L.add_rms_norm_linear(x, r, g, 1e-6, w)
     want_y, want_sum = path.add_norm_project(to_bits(x), to_bits(r), to_bits(g), 1e-6, to_bits(w))

@@ -199,6 +199,21 @@ def _stage_status(m, k, epilogue, t, kw, u, pro=False):
     return _native.FTK_OK if (t, k // (128 * kw), kw, u) in shapes else _native.FTK_ERR_INVALID
 
 
+#: (C, KW, D, pro) the RING kind is built for (NX follows M: 8 x rows up to M = 8, else 16)
+RING_SHAPES = ((4, 8, 2),)
+RING_LONG = ((12, 8, 2), (12, 8, 3))
+
+
+def _ring_status(m, k, epilogue, kw, d, pro=False):
+    if not 2 <= m <= 16 or k % (128 * kw):
+        return _native.FTK_ERR_UNSUPPORTED
+    c = k // (128 * kw)
+    shapes = RING_SHAPES + (RING_LONG if not pro and epilogue == _native.EPI_STORE else ())
+    if (c, kw, d) == (12, 8, 3) and m > 8:
+        return _native.FTK_ERR_INVALID  # three units of 16 x rows would not fit the LDS
+    return _native.FTK_OK if (c, kw, d) in shapes else _native.FTK_ERR_INVALID
+
+
 def _configs(m):
     gemv = []
     if m <= 4:
@@ -215,6 +230,9 @@ def _configs(m):
                  for rs, _, kw in QUAD_SHAPES + QUAD_ONE for gpc in (1, 8)]
         gemv += [_native.Config(_native.KIND_STAGE, 16 * t, u, gpc, kw)
                  for t, _, kw, u in STAGE_EVEN + STAGE_ONE + STAGE_LONG for gpc in (1, 4)]
+    if 2 <= m <= 16:
+        gemv += [_native.Config(_native.KIND_RING, 16, d, gpc, kw) for _, kw, d in RING_SHAPES + RING_LONG
+                 for gpc in (1, 4)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
             for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
     return [None] + gemv + mfma
@@ -258,6 +276,11 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert status == want, (m, n, k, epilogue, cfg)
                 if want != _native.FTK_OK:
                     continue
+            if cfg is not None and cfg.kind == _native.KIND_RING:
+                want = _ring_status(m, k, epilogue, cfg.waves, cfg.unroll)
+                assert status == want, (m, n, k, epilogue, cfg)
+                if want != _native.FTK_OK:
+                    continue
             assert status == _native.FTK_OK, (m, n, k, epilogue, cfg)
             counts, max_row = _coverage(p, n, epilogue)
             assert np.all(counts == 1), (m, n, k, epilogue, cfg)
@@ -278,6 +301,13 @@ def test_plan_writes_every_output_once(m, n, k):
                 # any walk depth (the epilogue runs every 64 // (T KW) tiles); groups_per_cu workgroups per CU
                 gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else 1
                 assert 1 <= p.grid <= min(p.tiles, 256 * gpc)
+                assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
+            if p.kind == _native.KIND_RING:
+                # one workgroup per CU (groups_per_cu of them), 16 weight rows per tile, any walk depth
+                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else 1
+                assert 1 <= p.grid <= min(p.tiles, 256 * gpc) and p.rows_per_wave == 16
+                assert p.tiles == -(-(n // 2 if epilogue == _native.EPI_SWIGLU else n) //
+                                    (8 if epilogue == _native.EPI_SWIGLU else 16))
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_QUAD:
                 assert 1 <= p.grid <= p.tiles and -(-p.tiles // p.grid) <= 8
@@ -301,18 +331,27 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
-    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # 16x16x32 MFMA tiles fed through LDS
-    assert p.kind == _native.KIND_STAGE and p.threads == 512 and p.unroll == 2 and p.grid == 256
+    # 5..16 rows: weight and x segments loaded straight into LDS (RING), one workgroup per CU
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
+    assert p.kind == _native.KIND_RING and p.threads == 512 and p.unroll == 2 and p.grid == 256
     _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # with the norm
-    assert p.kind == _native.KIND_QUAD and p.rows_per_wave == 8 and p.waves == 8
-    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K: x streamed, 3 segments in flight
-    assert p.kind == _native.KIND_STAGE and p.waves == 8 and p.unroll == 3
-    _native.call("ftk_plan_project", 8, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)  # fused at 5..8: 4x4x4
-    assert p.kind == _native.KIND_QUAD and p.threads == 512 and p.rows_per_wave == 8
-    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_STAGE and p.rows_per_wave == 16 and p.grid == 192
-    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)
-    assert p.kind == _native.KIND_STAGE and p.unroll == 3
+    assert p.kind == _native.KIND_RING and p.rows_per_wave == 16 and p.waves == 8 and p.grid == 192
+    _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K: three units in flight
+    assert p.kind == _native.KIND_RING and p.waves == 8 and p.unroll == 3
+    _native.call("ftk_plan_project", 8, 24576, 4096, _native.EPI_SWIGLU | _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_RING and p.tiles == 12288 // 8 and p.grid == 256
+    _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # 16 x rows: two units fit
+    assert p.kind == _native.KIND_RING and p.unroll == 2
+    _native.call("ftk_plan_project", 5, 151936, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STAGE  # lm_head + argmax: level with RING, stays on STAGE
+    # the prologue's residual add is not a RING form: such calls plan as before
+    _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, None, p)
+    assert p.kind == _native.KIND_QUAD
+    _native.call("ftk_plan_project", 16, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, None, p)
+    assert p.kind == _native.KIND_STAGE
+    ring = _native.Config(_native.KIND_RING, 16, 2, 0, 8)
+    assert _native.lib().ftk_plan_project(5, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, ring,
+                                          p) == _native.FTK_OK  # an explicit RING plan is accepted; the call refuses
     c = _native.Config(_native.KIND_MFMA_STREAM, 0, 0, 0, 0)  # x streamed beside the weights
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, c, p)
     assert p.kind == _native.KIND_MFMA_STREAM and p.waves == 8 and p.unroll == 16
@@ -328,10 +367,10 @@ def test_plan_kinds():
 
 
 def test_default_kind_for_8b_shapes():
-    """The planner's choice at the Qwen3-8B shapes (from the MI355X sweep): STREAM at M = 1 and,
-    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); QUAD for QKV at
-    M = 5..8; STAGE for the rest of 5..16 (the 8-row STREAM kernel where K = 12288 has the
-    prologue)."""
+    """The planner's choice at the Qwen3-8B shapes (from the MI355X sweeps): STREAM at M = 1 and,
+    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); RING for every
+    projection and SwiGLU at 5..16; STAGE for lm_head + argmax at 5..16 (the 8-row STREAM kernel
+    where K = 12288 has the prologue)."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -343,12 +382,14 @@ def test_default_kind_for_8b_shapes():
             quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
             if m < quad_early:
                 want = _native.KIND_STREAM
-            elif (m <= 8 and name == "qkv") or m <= 4:
+            elif m <= 4:
                 want = _native.KIND_QUAD
-            else:
+            elif name == "lm_head":
                 want = _native.KIND_STAGE
+            else:
+                want = _native.KIND_RING
             assert p.kind == want, (m, name, p.kind)
-    # the prologue at K = 12288 has no QUAD shape that fits the registers: the 8-row STREAM kernel
+    # the prologue at K = 12288 has no QUAD or RING shape: the 8-row STREAM kernel
     p = _native.Plan()
     _native.call("ftk_plan_project", 8, 4096, 12288, _native.PLAN_PROLOGUE, 256, None, p)
     assert p.kind == _native.KIND_STREAM and p.waves == 8 and p.threads == 512
