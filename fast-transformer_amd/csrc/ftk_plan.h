@@ -180,11 +180,14 @@ FTK_HD int ring_weight_row(int epi, int t, int r, int n_rows) {
   const int n = t * 16 + r;
   return n < n_rows ? n : n_rows - 1;
 }
-// LDS of a RING workgroup besides its per-tile partials: the ring (KW waves x D
-// units x (4 KiB of weights + NX KiB of x)), the gain (K BF16) with the
-// prologue, the argmax keys and the row scales.
+// 16-byte slots of one wave's ring: D units of 4 KiB of weights + NX KiB of x;
+// with C <= 4 (x kept in registers after the first tile) 16 KiB, which later
+// tiles use as four weight-only units.
+FTK_HD constexpr int ring_wave_slots(int c, int d, int nx) { return c <= 4 ? 4 * 256 : d * (256 + 64 * nx); }
+// LDS of a RING workgroup besides its per-tile partials: the rings, the gain (K
+// BF16) with the prologue, the argmax keys and the row scales.
 FTK_HD constexpr int ring_lds_fixed(int c, int kw, int d, int nx, bool pro) {
-  return kw * d * (256 + 64 * nx) * 16 + (pro ? 16 * c * kw * 16 : 16) + kw * 16 * 8 + 64;
+  return kw * ring_wave_slots(c, d, nx) * 16 + (pro ? 16 * c * kw * 16 : 16) + kw * 16 * 8 + 64;
 }
 // Tiles whose per-wave partials (KW KiB each) fit beside it in 160 KiB (at most 8).
 FTK_HD constexpr int ring_max_depth(int c, int kw, int d, int nx, bool pro) {

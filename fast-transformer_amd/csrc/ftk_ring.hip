@@ -33,8 +33,9 @@
 //     (their B operand is zero). Either way they feed only MFMA output columns
 //     >= M, which are never stored.
 //   * With C <= 4 the first tile's B operands (normalised, with the prologue)
-//     stay in registers and later tiles load weights only; otherwise x is
-//     loaded with every unit.
+//     stay in registers and later tiles load weights only, into 4 KiB slots:
+//     a wave's 16 KiB then hold all four units of the next tile in flight
+//     while it reads the current one. Otherwise x is loaded with every unit.
 //   * RMSNorm prologue: a pre-pass reads the x rows (or the gathered rows)
 //     row-contiguously for their sums of squares (wave w: rows w, w + KW, ...;
 //     lanes in chunk order, the DPP tree, one barrier) and workgroup 0 stores
@@ -149,11 +150,13 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   static_assert(NX == 2 || NX == 4, "x rows per unit: 8 or 16");
   constexpr bool XREG = C <= 4;                     // B operands kept after the first tile
   constexpr int XS = 64 * NX;                       // x slots (16 bytes) per unit
-  constexpr int SLOT = 256 + XS;                    // slots per unit
+  constexpr int SLOT = 256 + XS;                    // 16-byte slots per unit with x
+  constexpr int RW = ring_wave_slots(C, D, NX);     // 16-byte slots of one wave's ring
+  static_assert(!XREG || (C == 4 && D == 2 && RW == 4 * 256), "the walk below is written for C = 4, D = 2");
   constexpr int DMAX = ring_max_depth(C, KW, D, NX, PRO);
   static_assert(DMAX >= 1, "the ring leaves no LDS for the partials");
   constexpr int GCH = PRO ? 16 * C * KW : 1;        // 16-byte chunks of the gain (K / 8)
-  __shared__ u32x4_t ring[KW][D][SLOT];
+  __shared__ u32x4_t ring[KW][RW];
   __shared__ f32x4_t part[DMAX][KW][64];
   __shared__ u32x4_t gain[GCH];
   __shared__ float red[16];
@@ -182,8 +185,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     xrow[q] = PRO ? x_row(a, r) : a.x + (size_t)r * K;
     x_off[q] = 8 * ((lane & 15) ^ ring_swz(row));
   }
-  auto issue = [&](int t, int j, int slot, bool with_x) {
-    u32x4_t* dst = ring[kw][slot];
+  auto issue = [&](int t, int j, u32x4_t* dst, bool with_x) {
     const size_t k0 = seg0 + (size_t)j * KW * 128;
     if (with_x) {
 #pragma unroll
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   // ---- the first D units (all of the first tile: D <= C) ----------------------
   asm volatile("" ::: "memory");  // keep the prologue's loads ahead of the units (the count below)
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(wg, d, d, true);
+  for (int d = 0; d < D; ++d) issue(wg, d, ring[kw] + d * SLOT, true);
 
   // ---- RMSNorm prologue, part 2: row scales while the first units stream -------
   float scale = 0.f;
@@ -337,64 +339,43 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   const bool x_real = li < 4 * NX;
   u32x4_t xr[XREG ? C : 1][4];
   int count = 0, done = 0;
-  for (int i = 0; i < my_tiles; ++i) {
-    const int tile = wg + i * G;
-    const bool first = i == 0;
-    const bool more = i + 1 < my_tiles;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    static_for<0, C>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      constexpr int slot = j % D;
-      // Units issued after this one: the rest of the ring in this tile, then
-      // (with more tiles) the first units of the next one.
-      constexpr int n_same = (D - 1) < (C - 1 - j) ? (D - 1) : (C - 1 - j);
-      constexpr int n_next = (D - 1) - n_same;
-      constexpr int later_x = XREG ? 0 : NX;  // x loads of a unit of a later tile
-      constexpr int w_first_more = n_same * (4 + NX) + n_next * (4 + later_x);
-      constexpr int w_first_last = n_same * (4 + NX);
-      constexpr int w_later_more = n_same * (4 + later_x) + n_next * (4 + later_x);
-      constexpr int w_later_last = n_same * (4 + later_x);
-      if (first) {
-        if (more) wait_vm<w_first_more>(); else wait_vm<w_first_last>();
-      } else {
-        if (more) wait_vm<w_later_more>(); else wait_vm<w_later_last>();
-      }
-      const u32x4_t* u = ring[kw][slot];
-      const size_t kseg = seg0 + (size_t)j * KW * 128;
-      // One unit's operands: weights [0, 4), x [4, 8), gain [8, 12).
-      constexpr int NOPS = PRO ? 12 : 8;
-      u32x4_t op[NOPS];
-      const bool fresh = !XREG || first;  // B operands come from this unit's x
+  // One unit at u (segment J of the current tile): read it into registers, refill
+  // (the slot's contents are in registers, so the next load is not held back by
+  // the normalisation and the MFMAs), then the four MFMAs. `fresh`: the B
+  // operands come from this unit's x (normalised with the prologue) and, with
+  // XREG, are kept for the later tiles.
+  auto unit = [&](const u32x4_t* u, auto J, bool fresh, f32x4_t& acc, auto&& refill) {
+    constexpr int j = decltype(J)::value;
+    const size_t kseg = seg0 + (size_t)j * KW * 128;
+    constexpr int NOPS = PRO ? 12 : 8;  // weights [0, 4), x [4, 8), gain [8, 12)
+    u32x4_t op[NOPS];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int at = rd + ((4 * s + g) ^ hs);
-        op[s] = lds_read16(u + at);
-        if (fresh) {
-          op[4 + s] = lds_read16(u + 256 + (x_real ? at : 0));
-          if constexpr (PRO) op[8 + s] = lds_read16(gain + ((kseg + 32 * s + 8 * g) >> 3));
-        }
+    for (int s = 0; s < 4; ++s) {
+      const int at = rd + ((4 * s + g) ^ hs);
+      op[s] = lds_read16(u + at);
+      if (fresh) {
+        op[4 + s] = lds_read16(u + 256 + (x_real ? at : 0));
+        if constexpr (PRO) op[8 + s] = lds_read16(gain + ((kseg + 32 * s + 8 * g) >> 3));
       }
-      lds_ready(op);
-      // The slot's contents are in registers: refill it before the arithmetic,
-      // so the next load is not held back by the normalisation and the MFMAs.
-      if constexpr (j + D < C) {
-        issue(tile, j + D, slot, first || !XREG);
-      } else {
-        if (more) issue(tile + G, j + D - C, slot, !XREG);
-      }
+    }
+    lds_ready(op);
+    refill();
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        u32x4_t b;
-        if (fresh) {
-          b = x_real ? op[4 + s] : u32x4_t{0u, 0u, 0u, 0u};
-          if constexpr (PRO) b = norm8(b, op[8 + s], scale);
-          if constexpr (XREG) xr[j][s] = b;
-        } else {
-          b = xr[XREG ? j : 0][s];
-        }
-        acc = mfma16x16x32(op[s], b, acc);
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t b;
+      if (fresh) {
+        b = x_real ? op[4 + s] : u32x4_t{0u, 0u, 0u, 0u};
+        if constexpr (PRO) b = norm8(b, op[8 + s], scale);
+        if constexpr (XREG) xr[j][s] = b;
+      } else {
+        b = xr[XREG ? j : 0][s];
       }
-    });
+      acc = mfma16x16x32(op[s], b, acc);
+    }
+  };
+  // Park a finished tile's partials; every DMAX tiles (and after the last) the
+  // workgroup sums them and runs their epilogue. Returns false after the last.
+  auto park = [&](const f32x4_t& acc, bool more) {
     part[count][kw][lane] = acc;
     ++count;
     if (count == DMAX || !more) {  // workgroup-uniform: every wave walks the same tiles
@@ -402,8 +383,85 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       flush(count, done);
       done += count;
       count = 0;
-      if (!more) break;
+      if (!more) return false;
       lds_barrier();  // the next tiles park in the same slots
+    }
+    return true;
+  };
+
+  if constexpr (XREG) {
+    // First tile: units of x and weights, two in flight, in the two x-sized slots
+    // at 0 and SLOT. From its third unit on, the wave's 16 KiB are four
+    // weight-only slots q0..q3 (4 KiB each) and the next tile's units go there,
+    // all four in flight: unit 0 once slot 0 is free (with 16 x rows, unit 1 too,
+    // slot 0 covering q0 and q1), the rest once slot 1 is.
+    const bool more0 = my_tiles > 1;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    static_for<0, C>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      constexpr int early = NX == 2 ? 1 : 2;  // next-tile units issued after unit C - 2
+      if constexpr (j < C - 1) {
+        wait_vm<4 + NX>();
+      } else {
+        if (more0) wait_vm<4 * early>(); else wait_vm<0>();
+      }
+      unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
+        if constexpr (j + 2 < C) {
+          issue(wg, j + 2, ring[kw] + (j % 2) * SLOT, true);
+        } else if constexpr (j == C - 2) {
+          if (more0) {
+#pragma unroll
+            for (int q = 0; q < early; ++q) issue(wg + G, q, ring[kw] + 256 * q, false);
+          }
+        } else {
+          if (more0) {
+#pragma unroll
+            for (int q = early; q < 4; ++q) issue(wg + G, q, ring[kw] + 256 * q, false);
+          }
+        }
+      });
+    });
+    if (park(acc, more0)) {
+      // Later tiles: unit j of tile i sits in q_j; after reading it, unit j of
+      // tile i + 1 takes its place, so the next tile is in flight in full.
+      for (int i = 1; i < my_tiles; ++i) {
+        const int tile = wg + i * G;
+        const bool more = i + 1 < my_tiles;
+        f32x4_t acc2 = {0.f, 0.f, 0.f, 0.f};
+        static_for<0, C>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
+          if (more) wait_vm<4 * (C - 1)>(); else wait_vm<4 * (C - 1 - j)>();
+          unit(ring[kw] + 256 * j, J, false, acc2, [&] {
+            if (more) issue(tile + G, j, ring[kw] + 256 * j, false);
+          });
+        });
+        if (!park(acc2, more)) break;
+      }
+    }
+  } else {
+    // x travels with every unit: D units in flight in D slots of SLOT.
+    for (int i = 0; i < my_tiles; ++i) {
+      const int tile = wg + i * G;
+      const bool more = i + 1 < my_tiles;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      static_for<0, C>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        constexpr int slot = j % D;
+        // Units issued after this one: the rest of the ring in this tile, then
+        // (with more tiles) the first units of the next one; NX + 4 loads each.
+        constexpr int n_same = (D - 1) < (C - 1 - j) ? (D - 1) : (C - 1 - j);
+        constexpr int n_next = (D - 1) - n_same;
+        if (more) wait_vm<(n_same + n_next) * (4 + NX)>(); else wait_vm<n_same * (4 + NX)>();
+        unit(ring[kw] + slot * SLOT, J, true, acc, [&] {
+          if constexpr (j + D < C) {
+            issue(tile, j + D, ring[kw] + slot * SLOT, true);
+          } else {
+            if (more) issue(tile + G, j + D - C, ring[kw] + slot * SLOT, true);
+          }
+        });
+      });
+      if (!park(acc, more)) break;
     }
   }
 
