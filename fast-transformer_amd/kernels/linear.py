@@ -346,6 +346,12 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
         best_us = _cold_us(lambda w: run(best, w), weights)
         if best_us >= native_us * 0.985:
             best = "native"
+    if best not in ("native", None):
+        # the same recheck against the planner default: a launch shape must keep its 1.5 % lead
+        # over it on a second timing, or the default stays (timing noise does not switch kernels)
+        default_us = _cold_us(lambda w: run(None, w), weights)
+        if _cold_us(lambda w: run(best, w), weights) >= default_us * 0.985:
+            best = None
     validated.sort(key=lambda item: item[0])
     _VALIDATED[key] = validated
     del weights
