@@ -186,22 +186,25 @@ static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64
 
 // RING launch shape: 8 waves split K; two units in flight, three for the long K
 // (K = 12288) at up to 8 rows, where they fit the LDS.
+// lm_head + argmax (thousands of tiles) walks them in two rounds of workgroups:
+// 186.6 us at 5 rows against 188.7 with one round (and 188.3-189.0 for STAGE).
 struct RingDefault {
-  int kw, depth;
+  int kw, depth, groups_per_cu;
 };
 static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
-  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
   const int c = quad_segments((int)K, 8);
-  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2}, {8, 2}};
+  const int gpc = epi == FTK_EPI_ARGMAX ? 2 : 1;
+  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2, gpc}, {8, 2, gpc}};
   for (const RingDefault& d : order)
     if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro)) return d;
-  return {0, 0};
+  return {0, 0, 0};
 }
 // Where RING beats the other kinds (MI355X, Qwen3-8B shapes, 5..16 rows): every
-// projection and SwiGLU, with or without the norm prologue; lm_head + argmax is
-// level with STAGE and stays there. Not with the prologue's residual add, which
-// RING does not take (project_impl plans such calls without it).
-static bool ring_preferred(int64_t M, int epi) { return M >= 5 && epi != FTK_EPI_ARGMAX; }
+// projection, SwiGLU and lm_head + argmax, with or without the norm prologue.
+// Not with the prologue's residual add, which RING does not take (project_impl
+// plans such calls without it).
+static bool ring_preferred(int64_t M, int epi) { (void)epi; return M >= 5; }
 
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
@@ -366,8 +369,9 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->waves = kw;
     p->threads = 64 * kw;
     p->tiles = ring_tiles(epi, (int)N);
-    // One workgroup per CU (its LDS fills the CU), each walking its share.
-    const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : 1) * cus;
+    // One workgroup per CU at a time (its LDS fills the CU), each walking its
+    // share; lm_head + argmax in two rounds.
+    const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : (d.groups_per_cu ? d.groups_per_cu : 1)) * cus;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     return FTK_OK;

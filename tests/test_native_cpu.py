@@ -304,7 +304,8 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_RING:
                 # one workgroup per CU (groups_per_cu of them), 16 weight rows per tile, any walk depth
-                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else 1
+                default_gpc = 2 if epilogue == _native.EPI_ARGMAX else 1  # lm_head: two rounds
+                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else default_gpc
                 assert 1 <= p.grid <= min(p.tiles, 256 * gpc) and p.rows_per_wave == 16
                 assert p.tiles == -(-(n // 2 if epilogue == _native.EPI_SWIGLU else n) //
                                     (8 if epilogue == _native.EPI_SWIGLU else 16))
@@ -343,7 +344,7 @@ def test_plan_kinds():
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # 16 x rows: two units fit
     assert p.kind == _native.KIND_RING and p.unroll == 2
     _native.call("ftk_plan_project", 5, 151936, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_STAGE  # lm_head + argmax: level with RING, stays on STAGE
+    assert p.kind == _native.KIND_RING and p.tiles == 9496 and p.grid == 500  # lm_head: two rounds
     # the prologue's residual add is not a RING form: such calls plan as before
     _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, None, p)
     assert p.kind == _native.KIND_QUAD
@@ -369,8 +370,8 @@ def test_plan_kinds():
 def test_default_kind_for_8b_shapes():
     """The planner's choice at the Qwen3-8B shapes (from the MI355X sweeps): STREAM at M = 1 and,
     to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); RING for every
-    projection and SwiGLU at 5..16; STAGE for lm_head + argmax at 5..16 (the 8-row STREAM kernel
-    where K = 12288 has the prologue)."""
+    projection, SwiGLU and lm_head + argmax at 5..16 (the 8-row STREAM kernel where K = 12288 has
+    the prologue)."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -384,8 +385,6 @@ def test_default_kind_for_8b_shapes():
                 want = _native.KIND_STREAM
             elif m <= 4:
                 want = _native.KIND_QUAD
-            elif name == "lm_head":
-                want = _native.KIND_STAGE
             else:
                 want = _native.KIND_RING
             assert p.kind == want, (m, name, p.kind)
