@@ -188,17 +188,25 @@ static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64
 // (K = 12288) at up to 8 rows, where they fit the LDS.
 // lm_head + argmax (thousands of tiles) walks them in two rounds of workgroups:
 // 186.6 us at 5 rows against 188.7 with one round (and 188.3-189.0 for STAGE).
+// 24-row tiles where 16-row ones would leave a partial round of workgroups and
+// 24-row ones fill the CUs once (N = 6144 on 256 CUs: 256 tiles), without the
+// prologue: 10.45 / 10.56 us against 10.64 / 11.07 at M = 5 / 8. With the
+// prologue the 16-row tiles' second tile, run from registers and four units
+// deep, wins (10.94 / 11.44 against 11.76 / 11.60).
 struct RingDefault {
-  int kw, depth, groups_per_cu;
+  int kw, depth, groups_per_cu, rows;
 };
-static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K) {
-  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0};
+static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K, int cus) {
+  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0, 0};
   const int c = quad_segments((int)K, 8);
   const int gpc = epi == FTK_EPI_ARGMAX ? 2 : 1;
-  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2, gpc}, {8, 2, gpc}};
+  const int t16 = ring_tiles(epi, (int)N, 16), t24 = ring_tiles(epi, (int)N, 24);
+  const bool wide = epi == FTK_EPI_STORE && !pro && t16 > cus && t16 < 2 * cus && t24 <= cus &&
+                    ring_supported((int)M, (int)K, 8, 2, epi, pro, 24);
+  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2, gpc, wide ? 24 : 16}, {8, 2, gpc, 16}};
   for (const RingDefault& d : order)
-    if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro)) return d;
-  return {0, 0, 0};
+    if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro, d.rows)) return d;
+  return {0, 0, 0, 0};
 }
 // Where RING beats the other kinds (MI355X, Qwen3-8B shapes, 5..16 rows): every
 // projection, SwiGLU and lm_head + argmax, with or without the norm prologue.
@@ -230,7 +238,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // the shape.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     const bool stage = M >= 5 && stage_default(M, epi, pro, N, K).t != 0;
-    const bool ring = ring_ok && ring_preferred(M, epi) && ring_default(M, epi, pro, N, K).kw != 0;
+    const bool ring = ring_ok && ring_preferred(M, epi) && ring_default(M, epi, pro, N, K, cus).kw != 0;
     if (K % 8)
       kind = FTK_KIND_GENERIC;
     else if (ring)
@@ -358,17 +366,18 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   }
   if (kind == FTK_KIND_RING) {
     if (M < 2 || M > kRingMaxRows) return FTK_ERR_UNSUPPORTED;
-    const RingDefault d = ring_default(M, epi, pro, N, K);
+    const RingDefault d = ring_default(M, epi, pro, N, K, cus);
     const int kw = cfg && cfg->waves ? cfg->waves : (d.kw ? d.kw : 8);
     const int depth = cfg && cfg->unroll ? cfg->unroll : (d.depth ? d.depth : 2);
-    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 16;
+    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : (d.rows ? d.rows : 16);
     if (quad_segments((int)K, kw) == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
-    if (rows != 16 || !ring_supported((int)M, (int)K, kw, depth, epi, pro)) return FTK_ERR_INVALID;
+    if ((rows != 16 && rows != 24) || !ring_supported((int)M, (int)K, kw, depth, epi, pro, rows))
+      return FTK_ERR_INVALID;
     p->rows_per_wave = rows;
     p->unroll = depth;
     p->waves = kw;
     p->threads = 64 * kw;
-    p->tiles = ring_tiles(epi, (int)N);
+    p->tiles = ring_tiles(epi, (int)N, rows);
     // One workgroup per CU at a time (its LDS fills the CU), each walking its
     // share; lm_head + argmax in two rounds.
     const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : (d.groups_per_cu ? d.groups_per_cu : 1)) * cus;
@@ -612,11 +621,12 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
   if (p->kind == FTK_KIND_RING) {
     // Workgroup b walks tiles b + i grid; unit rows 0..15 of a tile.
     if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
-    const int per = ring_out_per_tile(epilogue);
+    const int rt = p->rows_per_wave;
+    const int per = ring_out_per_tile(epilogue, rt);
     for (int b = 0; b < p->grid; ++b)
       for (int tile = b; tile < p->tiles; tile += p->grid) {
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = ring_weight_row(epilogue, tile, r, (int)N);
+        for (int r = 0; r < rt; ++r) {
+          const int64_t row = ring_weight_row(epilogue, tile, r, (int)N, rt);
           if (row > *max_row) *max_row = row;
         }
         for (int r = 0; r < per; ++r) {
@@ -738,7 +748,7 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
     StageShape g = {p.rows_per_wave / 16, p.unroll, p.waves, p.grid, p.tiles};
     e = launch_stage(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_RING) {
-    RingShape g = {p.unroll, p.waves, p.grid, p.tiles};
+    RingShape g = {p.unroll, p.waves, p.grid, p.tiles, p.rows_per_wave};
     e = launch_ring(a, epilogue, g, s);
   } else if (p.kind == FTK_KIND_GEMV) {
     GemvShape g = {p.rows_per_wave, p.unroll, p.waves, p.grid, p.tiles, (size_t)p.lds_bytes};

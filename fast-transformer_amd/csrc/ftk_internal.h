@@ -135,8 +135,9 @@ struct RingShape {
   int kw;        // waves per workgroup, splitting K
   int grid;      // workgroups; each walks tiles wg, wg + grid, ...
   int tiles;
+  int rows;      // RT: weight rows per tile (16, or 24)
 };
-bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro);
+bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows = 16);
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& shape, hipStream_t stream);
 
 // Launch shape of the MFMA kind.

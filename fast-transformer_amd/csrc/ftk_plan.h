@@ -155,44 +155,49 @@ FTK_HD constexpr int stage_max_depth(int t, int kw) { return (64 * 1024) / (t * 
 
 // ---- M = 2..16 with K = 128 C KW: the RING kind (direct-to-LDS loads) --------
 // Segments as the QUAD kind (wave kw reads the 128-wide K segments j KW + kw).
-// A tile is 16 weight rows: rows 16 t .. 16 t + 15, or for SwiGLU the gate rows
-// 8 t .. 8 t + 7 (unit rows 0..7) and the matching up rows (unit rows 8..15).
-// Workgroup b walks tiles b, b + grid, ...; after every ring_max_depth tiles
-// the workgroup sums their per-wave partials and runs their epilogue.
+// A tile is RT weight rows: rows RT t .. RT t + RT - 1 (RT = 16, or 24 where 16-row
+// tiles would leave a partial round of workgroups, e.g. N = 6144 on 256 CUs), or
+// for SwiGLU (RT = 16) the gate rows 8 t .. 8 t + 7 (unit rows 0..7) and the
+// matching up rows (unit rows 8..15). Workgroup b walks tiles b, b + grid, ...;
+// after every ring_max_depth tiles the workgroup sums their per-wave partials and
+// runs their epilogue.
 constexpr int kRingMaxRows = 16;
 // x rows one unit carries, in loads of 4 rows: 8 rows up to M = 8, else 16.
 FTK_HD constexpr int ring_x_loads(int m) { return m <= 8 ? 2 : 4; }
-FTK_HD constexpr int ring_out_per_tile(int epi) { return epi == EPI_SWIGLU ? 8 : 16; }
-FTK_HD int ring_tiles(int epi, int n_rows) {
-  const int per = ring_out_per_tile(epi);
+FTK_HD constexpr int ring_out_per_tile(int epi, int rt = 16) { return epi == EPI_SWIGLU ? 8 : rt; }
+FTK_HD int ring_tiles(int epi, int n_rows, int rt = 16) {
+  const int per = ring_out_per_tile(epi, rt);
   return (gemv_outputs(epi, n_rows) + per - 1) / per;
 }
-// XOR swizzle of a unit row's 16 chunks (a permutation of 0..15).
-FTK_HD constexpr int ring_swz(int row) { return 4 * (row & 3) + (row >> 2); }
-// Weight row of unit row r (0..15) in tile t, clamped in bounds.
-FTK_HD int ring_weight_row(int epi, int t, int r, int n_rows) {
+// XOR swizzle of a unit row's 16 chunks (a permutation of 0..15; rows 16..23 as 0..7).
+FTK_HD constexpr int ring_swz(int row) { return 4 * (row & 3) + ((row & 15) >> 2); }
+// Weight row of unit row r (0..RT-1) in tile t, clamped in bounds.
+FTK_HD int ring_weight_row(int epi, int t, int r, int n_rows, int rt = 16) {
   if (epi == EPI_SWIGLU) {
     const int half = n_rows / 2;
     int c = t * 8 + (r & 7);
     c = c < half ? c : half - 1;
     return r < 8 ? c : half + c;
   }
-  const int n = t * 16 + r;
+  const int n = t * rt + r;
   return n < n_rows ? n : n_rows - 1;
 }
-// 16-byte slots of one wave's ring: D units of 4 KiB of weights + NX KiB of x;
-// with C <= 4 (x kept in registers after the first tile) 16 KiB, which later
-// tiles use as four weight-only units.
-FTK_HD constexpr int ring_wave_slots(int c, int d, int nx) { return c <= 4 ? 4 * 256 : d * (256 + 64 * nx); }
+// 16-byte slots of one wave's ring: D units of RT/4 KiB of weights + NX KiB of x;
+// with 16-row tiles and C <= 4 (x kept in registers after the first tile) 16 KiB,
+// which later tiles use as four weight-only units.
+FTK_HD constexpr int ring_wave_slots(int c, int d, int nx, int rt = 16) {
+  return (c <= 4 && rt == 16) ? 4 * 256 : d * (16 * rt + 64 * nx);
+}
 // LDS of a RING workgroup besides its per-tile partials: the rings, the gain (K
 // BF16) with the prologue, the argmax keys and the row scales.
-FTK_HD constexpr int ring_lds_fixed(int c, int kw, int d, int nx, bool pro) {
-  return kw * ring_wave_slots(c, d, nx) * 16 + (pro ? 16 * c * kw * 16 : 16) + kw * 16 * 8 + 64;
+FTK_HD constexpr int ring_lds_fixed(int c, int kw, int d, int nx, bool pro, int rt = 16) {
+  return kw * ring_wave_slots(c, d, nx, rt) * 16 + (pro ? 16 * c * kw * 16 : 16) + kw * 16 * 8 + 64;
 }
-// Tiles whose per-wave partials (KW KiB each) fit beside it in 160 KiB (at most 8).
-FTK_HD constexpr int ring_max_depth(int c, int kw, int d, int nx, bool pro) {
-  const int avail = 160 * 1024 - 512 - ring_lds_fixed(c, kw, d, nx, pro);
-  const int depth = avail < 0 ? 0 : avail / (kw * 1024);
+// Tiles whose per-wave partials (KW KiB per 16-row subtile) fit beside it in
+// 160 KiB (at most 8).
+FTK_HD constexpr int ring_max_depth(int c, int kw, int d, int nx, bool pro, int rt = 16) {
+  const int avail = 160 * 1024 - 512 - ring_lds_fixed(c, kw, d, nx, pro, rt);
+  const int depth = avail < 0 ? 0 : avail / (kw * 1024 * ((rt + 15) / 16));
   return depth > 8 ? 8 : depth;
 }
 

@@ -16,7 +16,8 @@
 //
 // Layout and schedule:
 //   * A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows)
-//     over all of K. A workgroup is KW waves splitting K; wave kw owns the
+//     over all of K, or 24 (two MFMA subtiles, the second half used) where 16-row
+//     tiles would leave a partial round of workgroups. A workgroup is KW waves splitting K; wave kw owns the
 //     128-wide K segments j KW + kw (j < C, K = 128 C KW). A unit is one segment
 //     of one tile: 4 KiB of weights (4 loads of 4 rows x 256 bytes) and, while
 //     the B operand is not held in registers, 4 NX rows of x (NX loads).
@@ -87,16 +88,21 @@ __device__ __forceinline__ u32x4_t lds_read16(const u32x4_t* p) {
 }
 template <int N>
 __device__ __forceinline__ void lds_ready(u32x4_t (&v)[N]) {
-  static_assert(N == 4 || N == 8 || N == 12, "operand sets of one unit");
+  static_assert(N == 4 || N == 8 || N == 12 || N == 16, "operand sets of one unit");
   if constexpr (N == 4)
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3])::"memory");
   else if constexpr (N == 8)
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])::"memory");
-  else
+  else if constexpr (N == 12)
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
                    "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11])::"memory");
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
+                   "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]),
+                   "+v"(v[15])::"memory");
 }
 
 // Global loads and LDS accesses of the prologue, issued as inline assembly. The
@@ -144,20 +150,24 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 }  // namespace
 
-template <int C, int KW, int D, int NX, bool PRO, int EPI>
+template <int C, int KW, int D, int NX, bool PRO, int EPI, int RT>
 __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   static_assert(C % D == 0, "a tile's units must fill the ring exactly");
   static_assert(NX == 2 || NX == 4, "x rows per unit: 8 or 16");
-  constexpr bool XREG = C <= 4;                     // B operands kept after the first tile
+  static_assert(RT == 16 || (RT == 24 && EPI == EPI_STORE), "24-row tiles: the STORE epilogue");
+  constexpr int SUB = (RT + 15) / 16;               // 16-row MFMA subtiles per tile
+  constexpr int WL = RT / 4;                        // weight loads per unit (4 rows each)
+  constexpr bool XREG = C <= 4 && RT == 16;         // B operands kept after the first tile
   constexpr int XS = 64 * NX;                       // x slots (16 bytes) per unit
-  constexpr int SLOT = 256 + XS;                    // 16-byte slots per unit with x
-  constexpr int RW = ring_wave_slots(C, D, NX);     // 16-byte slots of one wave's ring
+  constexpr int WS = 16 * RT;                       // weight slots (16 bytes) per unit
+  constexpr int SLOT = WS + XS;                     // 16-byte slots per unit with x
+  constexpr int RW = ring_wave_slots(C, D, NX, RT);  // 16-byte slots of one wave's ring
   static_assert(!XREG || (C == 4 && D == 2 && RW == 4 * 256), "the walk below is written for C = 4, D = 2");
-  constexpr int DMAX = ring_max_depth(C, KW, D, NX, PRO);
+  constexpr int DMAX = ring_max_depth(C, KW, D, NX, PRO, RT);
   static_assert(DMAX >= 1, "the ring leaves no LDS for the partials");
   constexpr int GCH = PRO ? 16 * C * KW : 1;        // 16-byte chunks of the gain (K / 8)
   __shared__ u32x4_t ring[KW][RW];
-  __shared__ f32x4_t part[DMAX][KW][64];
+  __shared__ f32x4_t part[DMAX][KW][SUB][64];
   __shared__ u32x4_t gain[GCH];
   __shared__ float red[16];
   __shared__ unsigned long long best_lds[KW][16];
@@ -172,11 +182,11 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   // ---- where this lane's loads go -------------------------------------------
   // Load q brings unit row 4 q + lane / 16; its chunk within the segment is
   // swizzled so that it lands in slot row * 16 + lane % 16.
-  int w_chunk[4];  // element offset of this lane's swizzled chunk in unit row 4 q + lane / 16
+  int w_chunk[WL];  // element offset of this lane's swizzled chunk in unit row 4 q + lane / 16
   int x_off[NX];
   const size_t seg0 = (size_t)kw * 128;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) w_chunk[q] = 8 * ((lane & 15) ^ ring_swz(4 * q + (lane >> 4)));
+  for (int q = 0; q < WL; ++q) w_chunk[q] = 8 * ((lane & 15) ^ ring_swz(4 * q + (lane >> 4)));
   const uint16_t* xrow[NX];
 #pragma unroll
   for (int q = 0; q < NX; ++q) {
@@ -189,11 +199,11 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     const size_t k0 = seg0 + (size_t)j * KW * 128;
     if (with_x) {
 #pragma unroll
-      for (int q = 0; q < NX; ++q) dma16<0>(xrow[q] + k0 + x_off[q], dst + 256 + 64 * q);
+      for (int q = 0; q < NX; ++q) dma16<0>(xrow[q] + k0 + x_off[q], dst + WS + 64 * q);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = ring_weight_row(EPI, t, 4 * q + (lane >> 4), a.N);
+    for (int q = 0; q < WL; ++q) {
+      const int row = ring_weight_row(EPI, t, 4 * q + (lane >> 4), a.N, RT);
       dma16<2>(a.w + (size_t)row * K + k0 + w_chunk[q], dst + 64 * q);
     }
   };
@@ -283,12 +293,12 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
         const int ll = e & 15, h = (e >> 4) & 1, i = e >> 5;
         if (ll >= M) continue;
         const int tl = wg + (done + i) * G;
-        f32x4_t s = part[i][0][h * 16 + ll];
-        f32x4_t u = part[i][0][(2 + h) * 16 + ll];
+        f32x4_t s = part[i][0][0][h * 16 + ll];
+        f32x4_t u = part[i][0][0][(2 + h) * 16 + ll];
 #pragma unroll
         for (int w = 1; w < KW; ++w) {
-          s += part[i][w][h * 16 + ll];
-          u += part[i][w][(2 + h) * 16 + ll];
+          s += part[i][w][0][h * 16 + ll];
+          u += part[i][w][0][(2 + h) * 16 + ll];
         }
         const int c0 = tl * 8 + 4 * h;
         uint16_t* yr = a.y + (size_t)ll * outputs;
@@ -297,16 +307,18 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
           if (c0 + r < outputs) yr[c0 + r] = (uint16_t)swiglu_bf16(s[r], u[r]);
       }
     } else {
-      const int entries = n * 64;
+      // Subtile sub holds unit rows 16 sub + 4 gg + r; with 24-row tiles the second
+      // subtile's rows past 23 are not the tile's.
+      const int entries = n * 64 * SUB;
       for (int e = tid; e < entries; e += 64 * KW) {
-        const int ln = e & 63, i = e >> 6;
+        const int ln = e & 63, sub = (e >> 6) % SUB, i = e / (64 * SUB);
         const int ll = ln & 15, gg = ln >> 4;
-        if (ll >= M) continue;
+        if (ll >= M || 16 * sub + 4 * gg >= RT) continue;
         const int tl = wg + (done + i) * G;
-        f32x4_t s = part[i][0][ln];
+        f32x4_t s = part[i][0][sub][ln];
 #pragma unroll
-        for (int w = 1; w < KW; ++w) s += part[i][w][ln];
-        const int n0 = tl * 16 + 4 * gg;
+        for (int w = 1; w < KW; ++w) s += part[i][w][sub][ln];
+        const int n0 = tl * RT + 16 * sub + 4 * gg;
         uint32_t bits[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -344,18 +356,24 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   // the normalisation and the MFMAs), then the four MFMAs. `fresh`: the B
   // operands come from this unit's x (normalised with the prologue) and, with
   // XREG, are kept for the later tiles.
-  auto unit = [&](const u32x4_t* u, auto J, bool fresh, f32x4_t& acc, auto&& refill) {
+  auto unit = [&](const u32x4_t* u, auto J, bool fresh, f32x4_t (&acc)[SUB], auto&& refill) {
     constexpr int j = decltype(J)::value;
     const size_t kseg = seg0 + (size_t)j * KW * 128;
-    constexpr int NOPS = PRO ? 12 : 8;  // weights [0, 4), x [4, 8), gain [8, 12)
+    // Operands: the weights of each subtile [4 sub, 4 sub + 4), x [XO, XO + 4), the gain after.
+    constexpr int XO = 4 * SUB;
+    constexpr int NOPS = XO + 4 + (PRO ? 4 : 0);
     u32x4_t op[NOPS];
+    // The second subtile of a 24-row tile reads unit rows 16 + (li & 7); its
+    // output rows past 23 are discarded.
+    const int r1 = 16 + (li & 7), rd1 = r1 * 16, hs1 = ring_swz(r1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int at = rd + ((4 * s + g) ^ hs);
       op[s] = lds_read16(u + at);
+      if constexpr (SUB == 2) op[4 + s] = lds_read16(u + rd1 + ((4 * s + g) ^ hs1));
       if (fresh) {
-        op[4 + s] = lds_read16(u + 256 + (x_real ? at : 0));
-        if constexpr (PRO) op[8 + s] = lds_read16(gain + ((kseg + 32 * s + 8 * g) >> 3));
+        op[XO + s] = lds_read16(u + WS + (x_real ? at : 0));
+        if constexpr (PRO) op[XO + 4 + s] = lds_read16(gain + ((kseg + 32 * s + 8 * g) >> 3));
       }
     }
     lds_ready(op);
@@ -364,19 +382,21 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     for (int s = 0; s < 4; ++s) {
       u32x4_t b;
       if (fresh) {
-        b = x_real ? op[4 + s] : u32x4_t{0u, 0u, 0u, 0u};
-        if constexpr (PRO) b = norm8(b, op[8 + s], scale);
+        b = x_real ? op[XO + s] : u32x4_t{0u, 0u, 0u, 0u};
+        if constexpr (PRO) b = norm8(b, op[XO + 4 + s], scale);
         if constexpr (XREG) xr[j][s] = b;
       } else {
         b = xr[XREG ? j : 0][s];
       }
-      acc = mfma16x16x32(op[s], b, acc);
+#pragma unroll
+      for (int t = 0; t < SUB; ++t) acc[t] = mfma16x16x32(op[4 * t + s], b, acc[t]);
     }
   };
   // Park a finished tile's partials; every DMAX tiles (and after the last) the
   // workgroup sums them and runs their epilogue. Returns false after the last.
-  auto park = [&](const f32x4_t& acc, bool more) {
-    part[count][kw][lane] = acc;
+  auto park = [&](const f32x4_t (&acc)[SUB], bool more) {
+#pragma unroll
+    for (int t = 0; t < SUB; ++t) part[count][kw][t][lane] = acc[t];
     ++count;
     if (count == DMAX || !more) {  // workgroup-uniform: every wave walks the same tiles
       lds_barrier();
@@ -396,7 +416,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     // all four in flight: unit 0 once slot 0 is free (with 16 x rows, unit 1 too,
     // slot 0 covering q0 and q1), the rest once slot 1 is.
     const bool more0 = my_tiles > 1;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[SUB] = {};
     static_for<0, C>([&](auto J) {
       constexpr int j = decltype(J)::value;
       constexpr int early = NX == 2 ? 1 : 2;  // next-tile units issued after unit C - 2
@@ -427,7 +447,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       for (int i = 1; i < my_tiles; ++i) {
         const int tile = wg + i * G;
         const bool more = i + 1 < my_tiles;
-        f32x4_t acc2 = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t acc2[SUB] = {};
         static_for<0, C>([&](auto J) {
           constexpr int j = decltype(J)::value;
           // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
@@ -444,15 +464,15 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     for (int i = 0; i < my_tiles; ++i) {
       const int tile = wg + i * G;
       const bool more = i + 1 < my_tiles;
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t acc[SUB] = {};
       static_for<0, C>([&](auto J) {
         constexpr int j = decltype(J)::value;
         constexpr int slot = j % D;
         // Units issued after this one: the rest of the ring in this tile, then
-        // (with more tiles) the first units of the next one; NX + 4 loads each.
+        // (with more tiles) the first units of the next one; WL + NX loads each.
         constexpr int n_same = (D - 1) < (C - 1 - j) ? (D - 1) : (C - 1 - j);
         constexpr int n_next = (D - 1) - n_same;
-        if (more) wait_vm<(n_same + n_next) * (4 + NX)>(); else wait_vm<n_same * (4 + NX)>();
+        if (more) wait_vm<(n_same + n_next) * (WL + NX)>(); else wait_vm<n_same * (WL + NX)>();
         unit(ring[kw] + slot * SLOT, J, true, acc, [&] {
           if constexpr (j + D < C) {
             issue(tile, j + D, ring[kw] + slot * SLOT, true);
@@ -483,46 +503,52 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 
 typedef void (*RingKernel)(ProjArgs, int);
 
-// Instantiated (C, KW, D, NX): K = 4096 (C = 4 at 8 waves, with or without the
-// prologue, every epilogue) with two units in flight; K = 12288 (C = 12, no
-// prologue, STORE) with two or three (three only for 8 x rows: 16 would not fit
-// the LDS). NX = 2 serves 2..8 rows, NX = 4 9..16.
-#define FTK_RING_SHAPE(C_, KW_, D_, NX_, PRO, EPI) \
-  if (c == C_ && kw == KW_ && d == D_ && nx == NX_) return ring_kernel<C_, KW_, D_, NX_, PRO, EPI>;
+// Instantiated (C, KW, D, NX, RT): K = 4096 (C = 4 at 8 waves, with or without the
+// prologue, every epilogue) with two units in flight, and 24-row tiles for the
+// STORE epilogue at up to 8 rows; K = 12288 (C = 12, no prologue, STORE) with two
+// or three (three only for 8 x rows: 16 would not fit the LDS). NX = 2 serves
+// 2..8 rows, NX = 4 9..16.
+#define FTK_RING_SHAPE(C_, KW_, D_, NX_, RT_, PRO, EPI) \
+  if (c == C_ && kw == KW_ && d == D_ && nx == NX_ && rt == RT_) return ring_kernel<C_, KW_, D_, NX_, PRO, EPI, RT_>;
 
 template <bool PRO, int EPI>
-static RingKernel pick_ring_shape(int c, int kw, int d, int nx) {
-  FTK_RING_SHAPE(4, 8, 2, 2, PRO, EPI)
-  FTK_RING_SHAPE(4, 8, 2, 4, PRO, EPI)
+static RingKernel pick_ring_shape(int c, int kw, int d, int nx, int rt) {
+  FTK_RING_SHAPE(4, 8, 2, 2, 16, PRO, EPI)
+  FTK_RING_SHAPE(4, 8, 2, 4, 16, PRO, EPI)
+  if constexpr (EPI == EPI_STORE) {
+    FTK_RING_SHAPE(4, 8, 2, 2, 24, PRO, EPI)
+  }
   if constexpr (!PRO && EPI == EPI_STORE) {
-    FTK_RING_SHAPE(12, 8, 2, 2, PRO, EPI)
-    FTK_RING_SHAPE(12, 8, 3, 2, PRO, EPI)
-    FTK_RING_SHAPE(12, 8, 2, 4, PRO, EPI)
+    FTK_RING_SHAPE(12, 8, 2, 2, 16, PRO, EPI)
+    FTK_RING_SHAPE(12, 8, 3, 2, 16, PRO, EPI)
+    FTK_RING_SHAPE(12, 8, 2, 4, 16, PRO, EPI)
   }
   return nullptr;
 }
 #undef FTK_RING_SHAPE
 
-static RingKernel pick_ring(int c, int kw, int d, int nx, bool pro, int epi) {
+static RingKernel pick_ring(int c, int kw, int d, int nx, int rt, bool pro, int epi) {
   switch (epi) {
-    case EPI_STORE: return pro ? pick_ring_shape<true, EPI_STORE>(c, kw, d, nx)
-                               : pick_ring_shape<false, EPI_STORE>(c, kw, d, nx);
-    case EPI_SWIGLU: return pro ? pick_ring_shape<true, EPI_SWIGLU>(c, kw, d, nx)
-                                : pick_ring_shape<false, EPI_SWIGLU>(c, kw, d, nx);
-    case EPI_ARGMAX: return pro ? pick_ring_shape<true, EPI_ARGMAX>(c, kw, d, nx)
-                                : pick_ring_shape<false, EPI_ARGMAX>(c, kw, d, nx);
+    case EPI_STORE: return pro ? pick_ring_shape<true, EPI_STORE>(c, kw, d, nx, rt)
+                               : pick_ring_shape<false, EPI_STORE>(c, kw, d, nx, rt);
+    case EPI_SWIGLU: return pro ? pick_ring_shape<true, EPI_SWIGLU>(c, kw, d, nx, rt)
+                                : pick_ring_shape<false, EPI_SWIGLU>(c, kw, d, nx, rt);
+    case EPI_ARGMAX: return pro ? pick_ring_shape<true, EPI_ARGMAX>(c, kw, d, nx, rt)
+                                : pick_ring_shape<false, EPI_ARGMAX>(c, kw, d, nx, rt);
   }
   return nullptr;
 }
 
-bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro) {
+bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows) {
   const int c = quad_segments(K, kw);
-  return M >= 2 && M <= kRingMaxRows && c > 0 && pick_ring(c, kw, depth, ring_x_loads(M), pro, epi) != nullptr;
+  return M >= 2 && M <= kRingMaxRows && c > 0 &&
+         pick_ring(c, kw, depth, ring_x_loads(M), rows, pro, epi) != nullptr;
 }
 
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& sh, hipStream_t stream) {
   const int c = quad_segments(a.K, sh.kw);
-  RingKernel k = c > 0 ? pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), a.gamma != nullptr, epi) : nullptr;
+  RingKernel k =
+      c > 0 ? pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi) : nullptr;
   if (k == nullptr || a.M < 2 || a.M > kRingMaxRows) return hipErrorInvalidValue;
   if (sh.grid < 1 || sh.grid > sh.tiles) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(sh.grid), dim3(64 * sh.kw), 0, stream, a, sh.tiles);

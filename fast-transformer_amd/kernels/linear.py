@@ -256,9 +256,10 @@ def _candidates(m, n, k, epilogue=_native.EPI_STORE, prologue=False):
                 for gpc in (1, 32):
                     configs.append((_native.KIND_QUAD, rows, 0, gpc, kw))
     if 2 <= m <= 16:
-        for depth in (2, 3):
-            for gpc in (1, 2):
-                configs.append((_native.KIND_RING, 16, depth, gpc, 8))
+        for rows in (16, 24):
+            for depth in (2, 3):
+                for gpc in (1, 2):
+                    configs.append((_native.KIND_RING, rows, depth, gpc, 8))
     if m >= 5:
         for rows in (16, 32):
             for unroll in (2, 3, 4):

@@ -32,8 +32,8 @@ def within(got_bits, want_bits):
     return bool(np.all(np.abs(g - w) <= ATOL + RTOL * np.abs(w)))
 
 
-def cfg(depth=2, gpc=0):
-    return _native.Config(_native.KIND_RING, 16, depth, gpc, 8)
+def cfg(depth=2, gpc=0, rows=16):
+    return _native.Config(_native.KIND_RING, rows, depth, gpc, 8)
 
 
 def _inputs(m, n, k, seed, device):
@@ -53,6 +53,25 @@ def test_store_matches_oracle(cuda, m):
     assert within(to_bits(L.rms_norm_linear(x, g, EPS, w, config=cfg())), path.norm_project(xb, gb, EPS, wb))
 
 
+@pytest.mark.parametrize("m", [2, 5, 8])
+@pytest.mark.parametrize("n", [6144, 1000 + 5, 24 * 300 + 17])
+def test_24_row_tiles_match_oracle(cuda, m, n):
+    """24-row tiles (two MFMA subtiles, the second half used), with and without the prologue; the
+    ragged last tile clamps its rows. Bit for bit the 16-row tiles' sums of the same rows."""
+    k = 4096
+    x, w, g = _inputs(m, n, k, seed=5050 + m + n, device=cuda)
+    xb, wb, gb = to_bits(x), to_bits(w), to_bits(g)
+    wide = cfg(rows=24)
+    p = L.plan(m, n, k, config=wide)
+    assert p.kind == _native.KIND_RING and p.rows_per_wave == 24 and p.tiles == -(-n // 24)
+    y = L.project(x, w, wide)
+    assert within(to_bits(y), path.project(xb, wb))
+    assert torch.equal(y, L.project(x, w, cfg()))
+    normed = L.rms_norm_linear(x, g, EPS, w, config=wide)
+    assert within(to_bits(normed), path.norm_project(xb, gb, EPS, wb))
+    assert torch.equal(normed, L.rms_norm_linear(x, g, EPS, w, config=cfg()))
+
+
 @pytest.mark.parametrize("m,depth", [(5, 2), (5, 3), (8, 3), (16, 2)])
 def test_long_k_matches_oracle(cuda, m, depth):
     """K = 12288 (the down projection): x travels with every unit."""
@@ -69,6 +88,9 @@ def test_shapes_the_ring_does_not_take_are_refused(cuda):
         status = _native.lib().ftk_plan_project(m, 4096, k, epilogue | (_native.PLAN_PROLOGUE if pro else 0),
                                                 256, cfg(depth), _native.Plan())
         assert status != _native.FTK_OK, (m, k, depth, pro)
+    for m, epilogue in ((9, _native.EPI_STORE), (5, _native.EPI_SWIGLU), (5, _native.EPI_ARGMAX)):
+        status = _native.lib().ftk_plan_project(m, 6144, 4096, epilogue, 256, cfg(rows=24), _native.Plan())
+        assert status != _native.FTK_OK, (m, epilogue)  # 24-row tiles: STORE at up to 8 x rows
 
 
 @pytest.mark.parametrize("m", [5, 16])
