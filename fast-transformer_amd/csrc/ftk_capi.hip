@@ -188,22 +188,31 @@ static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64
 // (K = 12288) at up to 8 rows, where they fit the LDS.
 // lm_head + argmax (thousands of tiles) walks them in two rounds of workgroups:
 // 186.6 us at 5 rows against 188.7 with one round (and 188.3-189.0 for STAGE).
-// 24-row tiles where 16-row ones would leave a partial round of workgroups and
-// 24-row ones fill the CUs once (N = 6144 on 256 CUs: 256 tiles), without the
-// prologue: 10.45 / 10.56 us against 10.64 / 11.07 at M = 5 / 8. With the
-// prologue the 16-row tiles' second tile, run from registers and four units
-// deep, wins (10.94 / 11.44 against 11.76 / 11.60).
+// Rows per tile (STORE): the fewest rows on the busiest CU, 16 first, then 12.
+// Where 16-row tiles leave a partial round of workgroups (N = 6144 on 256 CUs:
+// 384 tiles, so 192 workgroups walk two each), 12-row tiles fill every CU with
+// two, the second run from registers four units deep. QKV 6144 x 4096 on
+// MI355X, graphs of 36 distinct weights: with the prologue 10.83 / 10.88 /
+// 12.50 us at M = 5 / 8 / 16 against 11.36 / 11.44 / 12.74 with 16 rows; without
+// it 9.82 / 9.99 / 10.72 against 10.58 / 10.32 (24 rows) and 11.22 (16 rows).
+// 24-row tiles (one per CU there) stay a launch choice.
 struct RingDefault {
   int kw, depth, groups_per_cu, rows;
 };
+static int ring_busiest_rows(int tiles, int rt, int units) {
+  const int grid = persistent_programs(tiles, tiles < units ? tiles : units);
+  return grid > 0 ? (tiles + grid - 1) / grid * rt : 0;
+}
 static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K, int cus) {
   if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0, 0};
   const int c = quad_segments((int)K, 8);
   const int gpc = epi == FTK_EPI_ARGMAX ? 2 : 1;
-  const int t16 = ring_tiles(epi, (int)N, 16), t24 = ring_tiles(epi, (int)N, 24);
-  const bool wide = epi == FTK_EPI_STORE && !pro && t16 > cus && t16 < 2 * cus && t24 <= cus &&
-                    ring_supported((int)M, (int)K, 8, 2, epi, pro, 24);
-  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2, gpc, wide ? 24 : 16}, {8, 2, gpc, 16}};
+  int rows = 16;
+  if (epi == FTK_EPI_STORE && ring_supported((int)M, (int)K, 8, 2, epi, pro, 12) &&
+      ring_busiest_rows(ring_tiles(epi, (int)N, 12), 12, gpc * cus) <
+          ring_busiest_rows(ring_tiles(epi, (int)N, 16), 16, gpc * cus))
+    rows = 12;
+  const RingDefault order[] = {{8, c > 4 && M <= 8 ? 3 : 2, gpc, rows}, {8, 2, gpc, 16}};
   for (const RingDefault& d : order)
     if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro, d.rows)) return d;
   return {0, 0, 0, 0};
@@ -371,7 +380,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     const int depth = cfg && cfg->unroll ? cfg->unroll : (d.depth ? d.depth : 2);
     const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : (d.rows ? d.rows : 16);
     if (quad_segments((int)K, kw) == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
-    if ((rows != 16 && rows != 24) || !ring_supported((int)M, (int)K, kw, depth, epi, pro, rows))
+    if ((rows != 12 && rows != 16 && rows != 24) || !ring_supported((int)M, (int)K, kw, depth, epi, pro, rows))
       return FTK_ERR_INVALID;
     p->rows_per_wave = rows;
     p->unroll = depth;

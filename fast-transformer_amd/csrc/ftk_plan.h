@@ -182,11 +182,16 @@ FTK_HD int ring_weight_row(int epi, int t, int r, int n_rows, int rt = 16) {
   const int n = t * rt + r;
   return n < n_rows ? n : n_rows - 1;
 }
-// 16-byte slots of one wave's ring: D units of RT/4 KiB of weights + NX KiB of x;
-// with 16-row tiles and C <= 4 (x kept in registers after the first tile) 16 KiB,
-// which later tiles use as four weight-only units.
+// 16-byte slots of one wave's ring: D units of RT/4 KiB of weights + NX KiB of x.
+// With C <= 4 and tiles of at most 16 rows (x kept in registers after the first
+// tile) the ring holds the first tile's two units with x, or four weight-only
+// units for the later tiles; with fewer than 16 rows, the MFMA's unused rows past
+// the last unit read a pad (their outputs are never stored).
+FTK_HD constexpr int ring_xreg_slots(int nx, int rt) {
+  return (4 * 16 * rt > 2 * (16 * rt + 64 * nx) ? 4 * 16 * rt : 2 * (16 * rt + 64 * nx)) + 16 * (16 - rt);
+}
 FTK_HD constexpr int ring_wave_slots(int c, int d, int nx, int rt = 16) {
-  return (c <= 4 && rt == 16) ? 4 * 256 : d * (16 * rt + 64 * nx);
+  return (c <= 4 && rt <= 16) ? ring_xreg_slots(nx, rt) : d * (16 * rt + 64 * nx);
 }
 // LDS of a RING workgroup besides its per-tile partials: the rings, the gain (K
 // BF16) with the prologue, the argmax keys and the row scales.

@@ -154,15 +154,15 @@ template <int C, int KW, int D, int NX, bool PRO, int EPI, int RT>
 __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   static_assert(C % D == 0, "a tile's units must fill the ring exactly");
   static_assert(NX == 2 || NX == 4, "x rows per unit: 8 or 16");
-  static_assert(RT == 16 || (RT == 24 && EPI == EPI_STORE), "24-row tiles: the STORE epilogue");
+  static_assert(RT == 16 || ((RT == 24 || RT == 12) && EPI == EPI_STORE), "12- and 24-row tiles: the STORE epilogue");
   constexpr int SUB = (RT + 15) / 16;               // 16-row MFMA subtiles per tile
   constexpr int WL = RT / 4;                        // weight loads per unit (4 rows each)
-  constexpr bool XREG = C <= 4 && RT == 16;         // B operands kept after the first tile
+  constexpr bool XREG = C <= 4 && RT <= 16;         // B operands kept after the first tile
   constexpr int XS = 64 * NX;                       // x slots (16 bytes) per unit
   constexpr int WS = 16 * RT;                       // weight slots (16 bytes) per unit
   constexpr int SLOT = WS + XS;                     // 16-byte slots per unit with x
   constexpr int RW = ring_wave_slots(C, D, NX, RT);  // 16-byte slots of one wave's ring
-  static_assert(!XREG || (C == 4 && D == 2 && RW == 4 * 256), "the walk below is written for C = 4, D = 2");
+  static_assert(!XREG || (C == 4 && D == 2 && RW >= 4 * WS && RW >= 2 * SLOT), "the walk below is written for C = 4, D = 2");
   constexpr int DMAX = ring_max_depth(C, KW, D, NX, PRO, RT);
   static_assert(DMAX >= 1, "the ring leaves no LDS for the partials");
   constexpr int GCH = PRO ? 16 * C * KW : 1;        // 16-byte chunks of the gain (K / 8)
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   // ---- RMSNorm prologue, part 2: row scales while the first units stream -------
   float scale = 0.f;
   if constexpr (PRO) {
-    wait_vm<D * (4 + NX)>();  // the gain and x rows are in; the D units may still be in flight
+    wait_vm<D * (WL + NX)>();  // the gain and x rows are in; the D units may still be in flight
 #pragma unroll
     for (int i = 0; i < GPT; ++i) tie(gl[i]);
 #pragma unroll
@@ -411,19 +411,19 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 
   if constexpr (XREG) {
     // First tile: units of x and weights, two in flight, in the two x-sized slots
-    // at 0 and SLOT. From its third unit on, the wave's 16 KiB are four
-    // weight-only slots q0..q3 (4 KiB each) and the next tile's units go there,
-    // all four in flight: unit 0 once slot 0 is free (with 16 x rows, unit 1 too,
-    // slot 0 covering q0 and q1), the rest once slot 1 is.
+    // at 0 and SLOT. From its third unit on, the wave's ring holds four weight-only
+    // slots q0..q3 (RT / 4 KiB each) and the next tile's units go there, all four
+    // in flight: those wholly inside slot 0 (q0, and q1 too with 16 x rows) once
+    // slot 0 is free, the rest once slot 1 is.
     const bool more0 = my_tiles > 1;
     f32x4_t acc[SUB] = {};
     static_for<0, C>([&](auto J) {
       constexpr int j = decltype(J)::value;
-      constexpr int early = NX == 2 ? 1 : 2;  // next-tile units issued after unit C - 2
+      constexpr int early = SLOT / WS;  // next-tile units issued after unit C - 2
       if constexpr (j < C - 1) {
-        wait_vm<4 + NX>();
+        wait_vm<WL + NX>();
       } else {
-        if (more0) wait_vm<4 * early>(); else wait_vm<0>();
+        if (more0) wait_vm<WL * early>(); else wait_vm<0>();
       }
       unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
         if constexpr (j + 2 < C) {
@@ -431,12 +431,12 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
         } else if constexpr (j == C - 2) {
           if (more0) {
 #pragma unroll
-            for (int q = 0; q < early; ++q) issue(wg + G, q, ring[kw] + 256 * q, false);
+            for (int q = 0; q < early; ++q) issue(wg + G, q, ring[kw] + WS * q, false);
           }
         } else {
           if (more0) {
 #pragma unroll
-            for (int q = early; q < 4; ++q) issue(wg + G, q, ring[kw] + 256 * q, false);
+            for (int q = early; q < 4; ++q) issue(wg + G, q, ring[kw] + WS * q, false);
           }
         }
       });
@@ -451,9 +451,9 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
         static_for<0, C>([&](auto J) {
           constexpr int j = decltype(J)::value;
           // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
-          if (more) wait_vm<4 * (C - 1)>(); else wait_vm<4 * (C - 1 - j)>();
-          unit(ring[kw] + 256 * j, J, false, acc2, [&] {
-            if (more) issue(tile + G, j, ring[kw] + 256 * j, false);
+          if (more) wait_vm<WL * (C - 1)>(); else wait_vm<WL * (C - 1 - j)>();
+          unit(ring[kw] + WS * j, J, false, acc2, [&] {
+            if (more) issue(tile + G, j, ring[kw] + WS * j, false);
           });
         });
         if (!park(acc2, more)) break;
@@ -517,6 +517,8 @@ static RingKernel pick_ring_shape(int c, int kw, int d, int nx, int rt) {
   FTK_RING_SHAPE(4, 8, 2, 4, 16, PRO, EPI)
   if constexpr (EPI == EPI_STORE) {
     FTK_RING_SHAPE(4, 8, 2, 2, 24, PRO, EPI)
+    FTK_RING_SHAPE(4, 8, 2, 2, 12, PRO, EPI)
+    FTK_RING_SHAPE(4, 8, 2, 4, 12, PRO, EPI)
   }
   if constexpr (!PRO && EPI == EPI_STORE) {
     FTK_RING_SHAPE(12, 8, 2, 2, 16, PRO, EPI)

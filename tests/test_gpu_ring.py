@@ -72,6 +72,56 @@ def test_24_row_tiles_match_oracle(cuda, m, n):
     assert torch.equal(normed, L.rms_norm_linear(x, g, EPS, w, config=cfg()))
 
 
+@pytest.mark.parametrize("m", [2, 5, 8, 9, 16])
+@pytest.mark.parametrize("n", [6144, 1000 + 5, 12 * 300 + 7])
+def test_12_row_tiles_match_oracle(cuda, m, n):
+    """12-row tiles (one MFMA subtile, its last four rows unused; the second tile runs from
+    registers), with and without the prologue; the ragged last tile clamps its rows. Bit for bit
+    the 16-row tiles' sums of the same rows."""
+    k = 4096
+    x, w, g = _inputs(m, n, k, seed=5070 + m + n, device=cuda)
+    xb, wb, gb = to_bits(x), to_bits(w), to_bits(g)
+    narrow = cfg(rows=12)
+    p = L.plan(m, n, k, config=narrow)
+    assert p.kind == _native.KIND_RING and p.rows_per_wave == 12 and p.tiles == -(-n // 12)
+    y = L.project(x, w, narrow)
+    assert within(to_bits(y), path.project(xb, wb))
+    assert torch.equal(y, L.project(x, w, cfg()))
+    normed = L.rms_norm_linear(x, g, EPS, w, config=narrow)
+    assert within(to_bits(normed), path.norm_project(xb, gb, EPS, wb))
+    assert torch.equal(normed, L.rms_norm_linear(x, g, EPS, w, config=cfg()))
+    r = seeded((m, n), seed=5080 + m, device=cuda)
+    assert torch.equal(L.linear_residual(x, w, r, config=narrow), L.linear_residual(x, w, r, config=cfg()))
+
+
+def test_12_row_walks_and_graph_replays(cuda):
+    """12-row tiles walked far past the LDS depth by one workgroup (the epilogue inside the walk),
+    equal to short walks, and replayed from a captured graph bit for bit."""
+    m, n, k = 8, 12 * 2600 + 5, 4096
+    x, w, g = _inputs(m, n, k, seed=5090, device=cuda)
+    long_walks, short_walks = cfg(2, 1, rows=12), cfg(2, 16, rows=12)
+    p = L.plan(m, n, k, config=long_walks, prologue=True)
+    assert p.kind == _native.KIND_RING and -(-p.tiles // p.grid) > 8
+    got = L.rms_norm_linear(x, g, EPS, w, config=long_walks)
+    assert torch.equal(got, L.rms_norm_linear(x, g, EPS, w, config=short_walks))
+    assert within(to_bits(got), path.norm_project(to_bits(x), to_bits(g), EPS, to_bits(w)))
+    eager = to_bits(got).copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        L.rms_norm_linear(x, g, EPS, w, config=long_walks)
+        with torch.cuda.graph(graph, stream=stream):
+            out = L.rms_norm_linear(x, g, EPS, w, config=long_walks)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_bits(out), eager)
+
+
 @pytest.mark.parametrize("m,depth", [(5, 2), (5, 3), (8, 3), (16, 2)])
 def test_long_k_matches_oracle(cuda, m, depth):
     """K = 12288 (the down projection): x travels with every unit."""
@@ -91,6 +141,9 @@ def test_shapes_the_ring_does_not_take_are_refused(cuda):
     for m, epilogue in ((9, _native.EPI_STORE), (5, _native.EPI_SWIGLU), (5, _native.EPI_ARGMAX)):
         status = _native.lib().ftk_plan_project(m, 6144, 4096, epilogue, 256, cfg(rows=24), _native.Plan())
         assert status != _native.FTK_OK, (m, epilogue)  # 24-row tiles: STORE at up to 8 x rows
+    for m, epilogue, k in ((5, _native.EPI_SWIGLU, 4096), (5, _native.EPI_ARGMAX, 4096), (5, _native.EPI_STORE, 12288)):
+        status = _native.lib().ftk_plan_project(m, 6144, k, epilogue, 256, cfg(rows=12), _native.Plan())
+        assert status != _native.FTK_OK, (m, epilogue, k)  # 12-row tiles: STORE at K = 4096
 
 
 @pytest.mark.parametrize("m", [5, 16])

@@ -211,6 +211,9 @@ def _ring_status(m, k, epilogue, kw, d, pro=False, rows=16):
     if rows == 24:  # 24-row tiles: STORE, up to 8 x rows, C = 4
         ok = epilogue == _native.EPI_STORE and m <= 8 and (c, kw, d) == (4, 8, 2)
         return _native.FTK_OK if ok else _native.FTK_ERR_INVALID
+    if rows == 12:  # 12-row tiles: STORE, any row count, C = 4
+        ok = epilogue == _native.EPI_STORE and (c, kw, d) == (4, 8, 2)
+        return _native.FTK_OK if ok else _native.FTK_ERR_INVALID
     shapes = RING_SHAPES + (RING_LONG if not pro and epilogue == _native.EPI_STORE else ())
     if (c, kw, d) == (12, 8, 3) and m > 8:
         return _native.FTK_ERR_INVALID  # three units of 16 x rows would not fit the LDS
@@ -235,7 +238,7 @@ def _configs(m):
                  for t, _, kw, u in STAGE_EVEN + STAGE_ONE + STAGE_LONG for gpc in (1, 4)]
     if 2 <= m <= 16:
         gemv += [_native.Config(_native.KIND_RING, rows, d, gpc, kw) for _, kw, d in RING_SHAPES + RING_LONG
-                 for gpc in (1, 4) for rows in (16, 24)]
+                 for gpc in (1, 4) for rows in (12, 16, 24)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
             for rows, u, w in ((16, 4, 4), (16, 8, 8), (16, 4, 16), (32, 8, 4), (32, 4, 16), (64, 2, 8), (64, 4, 4))]
     return [None] + gemv + mfma
@@ -306,10 +309,10 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert 1 <= p.grid <= min(p.tiles, 256 * gpc)
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_RING:
-                # one workgroup per CU (groups_per_cu of them), 16 weight rows per tile, any walk depth
+                # one workgroup per CU (groups_per_cu of them), 12, 16 or 24 weight rows per tile, any walk depth
                 default_gpc = 2 if epilogue == _native.EPI_ARGMAX else 1  # lm_head: two rounds
                 gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else default_gpc
-                assert 1 <= p.grid <= min(p.tiles, 256 * gpc) and p.rows_per_wave in (16, 24)
+                assert 1 <= p.grid <= min(p.tiles, 256 * gpc) and p.rows_per_wave in (12, 16, 24)
                 assert p.tiles == -(-(n // 2 if epilogue == _native.EPI_SWIGLU else n) //
                                     (8 if epilogue == _native.EPI_SWIGLU else p.rows_per_wave))
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
@@ -338,14 +341,13 @@ def test_plan_kinds():
     # 5..16 rows: weight and x segments loaded straight into LDS (RING), one workgroup per CU
     _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
     assert p.kind == _native.KIND_RING and p.threads == 512 and p.unroll == 2 and p.grid == 256
-    # N = 6144: 24-row tiles, one per CU, where 16-row ones leave half a round -- without the norm;
-    # with it (QKV) the 16-row tiles' register-fed second tile wins
-    _native.call("ftk_plan_project", 5, 6144, 4096, 0, 256, None, p)
-    assert p.kind == _native.KIND_RING and p.rows_per_wave == 24 and p.waves == 8 and p.grid == 256
-    _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_RING and p.rows_per_wave == 16 and p.grid == 192
-    _native.call("ftk_plan_project", 16, 6144, 4096, 0, 256, None, p)  # 16 x rows: 16-row tiles
-    assert p.kind == _native.KIND_RING and p.rows_per_wave == 16 and p.grid == 192
+    # N = 6144: 12-row tiles, two per CU on every CU, where 16-row ones leave half a round (192
+    # workgroups walking two) -- with or without the norm, at any row count
+    for m, flags in ((5, 0), (5, _native.PLAN_PROLOGUE), (8, _native.PLAN_PROLOGUE), (16, 0)):
+        _native.call("ftk_plan_project", m, 6144, 4096, flags, 256, None, p)
+        assert p.kind == _native.KIND_RING and p.rows_per_wave == 12 and p.waves == 8 and p.grid == 256, (m, flags)
+    _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)  # N = 4096: one 16-row tile per CU
+    assert p.kind == _native.KIND_RING and p.rows_per_wave == 16 and p.grid == 256
     _native.call("ftk_plan_project", 8, 4096, 12288, 0, 256, None, p)  # long K: three units in flight
     assert p.kind == _native.KIND_RING and p.waves == 8 and p.unroll == 3
     _native.call("ftk_plan_project", 8, 24576, 4096, _native.EPI_SWIGLU | _native.PLAN_PROLOGUE, 256, None, p)
