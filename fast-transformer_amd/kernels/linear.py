@@ -256,7 +256,7 @@ def _candidates(m, n, k, epilogue=_native.EPI_STORE, prologue=False):
                 for gpc in (1, 32):
                     configs.append((_native.KIND_QUAD, rows, 0, gpc, kw))
     if 2 <= m <= 16:
-        for rows in (16, 24):
+        for rows in (12, 16, 24):
             for depth in (2, 3):
                 for gpc in (1, 2):
                     configs.append((_native.KIND_RING, rows, depth, gpc, 8))
