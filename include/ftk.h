@@ -92,8 +92,8 @@ typedef struct ftk_config {
   int rows_per_wave;   /* GEMV, STREAM: weight rows per row group per tile (1..8);
                           MFMA: rows per workgroup (16, 32, 64); MFMA_STREAM, STAGE: rows per tile
                           (16, 32); QUAD: weight rows per row group per tile (4, 8, 16, 24; SwiGLU
-                          8, 16, 24); RING: 16 (SwiGLU: 8 gate + 8 up rows), or 24 for
-                          the STORE epilogue at up to 8 rows */
+                          8, 16, 24); RING: 16 (SwiGLU: 8 gate + 8 up rows), or for the
+                          STORE epilogue 12 (at K = 4096), or 24 (at up to 8 rows) */
   int unroll;          /* GEMV: 16-byte chunks per lane per load batch (1, 2, 4);
                           MFMA: K steps of loads in flight per wave (T = 1, 2: 4 or 8; T = 4: 2 or 4);
                           STREAM, QUAD: unused (K fixes the chunks per lane);
