@@ -183,10 +183,16 @@ def tuned_graph(fn, rows, seconds, label):
     return capture(fn)
 
 
-def time_graph(graph, reps=10, inner=1):
-    """Median wall time of one replay, from HIP events on the replay stream (µs)."""
+def time_graph(graph, reps=10, inner=1, warm_s=0.0):
+    """Median wall time of one replay, from HIP events on the replay stream (µs). ``warm_s``: replay
+    untimed for that long first, so that the GPU's clocks have settled as they have mid-run."""
     graph.replay()
     torch.cuda.synchronize()
+    t_end = time.monotonic() + warm_s
+    while time.monotonic() < t_end:
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     times = []
     for _ in range(reps):
@@ -235,7 +241,7 @@ def planner_config(m, n, k, epilogue, prologue):
     return cfg
 
 
-def per_kind(step, kind, warm=2, config=None):
+def per_kind(step, kind, warm=2, config=None, warm_s=0.0):
     """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch.
     ``config`` pins the gate/up launch (otherwise each call takes its frozen choice)."""
     def fn():
@@ -256,7 +262,11 @@ def per_kind(step, kind, warm=2, config=None):
         _native.project_workspace(step.h.device, step.m, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU,
                                   prologue=True)
     graph = capture(fn, warm)
-    return time_graph(graph) / len(step.model.layers)
+    return time_graph(graph, warm_s=warm_s) / len(step.model.layers)
+
+
+#: Untimed replays before the roofline kernel's timed ones (seconds).
+ROOFLINE_WARM_S = 0.5
 
 
 def roofline(step):
@@ -267,7 +277,10 @@ def roofline(step):
     # the planner's default launch, pinned, so that --roofline-only (whose kernel trace backs this
     # figure) launches exactly the same kernel and grid whether or not this run selected shapes
     pinned = planner_config(1, 2 * cfg["inter"], cfg["hidden"], _native.EPI_SWIGLU, True)
-    gu_us = per_kind(step, "gate_up", warm=0, config=pinned)
+    # half a second of untimed replays first: the timed replays then see the clocks of a busy GPU,
+    # in the default run (after the step) and in --roofline-only alike; the last 10 replays (360
+    # launches) are the timed ones
+    gu_us = per_kind(step, "gate_up", warm=0, config=pinned, warm_s=ROOFLINE_WARM_S)
     gu_bytes = layer_bytes(cfg, 1)["gate_up"]
     return {"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(gu_bytes / gu_us / 1e3 / PEAK_GBS, 4), "traffic": load_traffic(),
@@ -442,7 +455,9 @@ def main():
     if args.roofline_only:
         model = Model(cfg, dev, head=False)
         roof = roofline(Step(model, 1, dev))
-        print(json.dumps({"mode": "roofline-only", "roofline": roof}), flush=True)
+        print(json.dumps({"mode": "roofline-only", "roofline": roof, "warm_s": ROOFLINE_WARM_S,
+                          "timed_launches": 10 * cfg["layers"], "note": "the timed launches are the last ones"}),
+              flush=True)
         return
     model = Model(cfg, dev)
     stage("Qwen3-8B weights resident")
