@@ -547,6 +547,10 @@ const char* ftk_status_string(int status) {
 int ftk_last_hip_error(void) { return g_last_hip_error; }
 
 int ftk_persistent_programs(int tiles, int units) { return persistent_programs(tiles, units); }
+int ftk_ring_tile(int wg, int step, int grid, int tiles) {
+  if (grid <= 0 || tiles <= 0 || wg < 0 || wg >= grid || step < 0 || wg + step * grid >= tiles) return -1;
+  return ring_tile(wg, step, grid, tiles);
+}
 
 int ftk_device_compute_units(void) {
   DeviceInfo d = device_info();

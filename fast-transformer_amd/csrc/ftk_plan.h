@@ -171,6 +171,18 @@ FTK_HD int ring_tiles(int epi, int n_rows, int rt = 16) {
 }
 // XOR swizzle of a unit row's 16 chunks (a permutation of 0..15; rows 16..23 as 0..7).
 FTK_HD constexpr int ring_swz(int row) { return 4 * (row & 3) + ((row & 15) >> 2); }
+// Tile of step i of RING workgroup wg in a grid of G over `tiles` tiles (steps
+// i < ceil((tiles - wg) / G)). The dispatcher deals workgroups to the 8 XCDs in
+// turn (wg on XCD wg % 8), so in every full round of G tiles each XCD's G / 8
+// workgroups take one contiguous run of G / 8 tiles; the round as a whole still
+// covers one contiguous range. A partial last round, and a grid that is not a
+// multiple of 8, keep tile wg + i G. (Measured on MI355X against wg + i G: O at
+// 5..16 rows 0.2-0.5 us faster, gate/up + SwiGLU at 16 rows 0.7 us; for STREAM's
+// thousands of short-lived workgroups the plain order is faster.)
+FTK_HD int ring_tile(int wg, int i, int G, int tiles) {
+  if ((G & 7) != 0 || (i + 1) * G > tiles) return wg + i * G;
+  return i * G + (G >> 3) * (wg & 7) + (wg >> 3);
+}
 // Weight row of unit row r (0..RT-1) in tile t, clamped in bounds.
 FTK_HD int ring_weight_row(int epi, int t, int r, int n_rows, int rt = 16) {
   if (epi == EPI_SWIGLU) {

@@ -176,7 +176,8 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   const int li = lane & 15, g = lane >> 4;  // MFMA layout: row li, k quarter g
   const int M = a.M, K = a.K;               // K == 128 C KW (checked by the planner)
   const int wg = blockIdx.x, G = gridDim.x;
-  const int my_tiles = (tiles - wg + G - 1) / G;  // tiles wg, wg + G, ... (grid <= tiles)
+  const int my_tiles = (tiles - wg + G - 1) / G;  // steps of this workgroup (grid <= tiles)
+  auto tile_at = [&](int i) { return ring_tile(wg, i, G, tiles); };
   const int outputs = gemv_outputs(EPI, a.N);
 
   // ---- where this lane's loads go -------------------------------------------
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   // ---- the first D units (all of the first tile: D <= C) ----------------------
   asm volatile("" ::: "memory");  // keep the prologue's loads ahead of the units (the count below)
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(wg, d, ring[kw] + d * SLOT, true);
+  for (int d = 0; d < D; ++d) issue(tile_at(0), d, ring[kw] + d * SLOT, true);
 
   // ---- RMSNorm prologue, part 2: row scales while the first units stream -------
   float scale = 0.f;
@@ -292,7 +293,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       for (int e = tid; e < entries; e += 64 * KW) {
         const int ll = e & 15, h = (e >> 4) & 1, i = e >> 5;
         if (ll >= M) continue;
-        const int tl = wg + (done + i) * G;
+        const int tl = tile_at(done + i);
         f32x4_t s = part[i][0][0][h * 16 + ll];
         f32x4_t u = part[i][0][0][(2 + h) * 16 + ll];
 #pragma unroll
@@ -314,7 +315,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
         const int ln = e & 63, sub = (e >> 6) % SUB, i = e / (64 * SUB);
         const int ll = ln & 15, gg = ln >> 4;
         if (ll >= M || 16 * sub + 4 * gg >= RT) continue;
-        const int tl = wg + (done + i) * G;
+        const int tl = tile_at(done + i);
         f32x4_t s = part[i][0][sub][ln];
 #pragma unroll
         for (int w = 1; w < KW; ++w) s += part[i][w][sub][ln];
@@ -427,16 +428,16 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       }
       unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
         if constexpr (j + 2 < C) {
-          issue(wg, j + 2, ring[kw] + (j % 2) * SLOT, true);
+          issue(tile_at(0), j + 2, ring[kw] + (j % 2) * SLOT, true);
         } else if constexpr (j == C - 2) {
           if (more0) {
 #pragma unroll
-            for (int q = 0; q < early; ++q) issue(wg + G, q, ring[kw] + WS * q, false);
+            for (int q = 0; q < early; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
           }
         } else {
           if (more0) {
 #pragma unroll
-            for (int q = early; q < 4; ++q) issue(wg + G, q, ring[kw] + WS * q, false);
+            for (int q = early; q < 4; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
           }
         }
       });
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       // Later tiles: unit j of tile i sits in q_j; after reading it, unit j of
       // tile i + 1 takes its place, so the next tile is in flight in full.
       for (int i = 1; i < my_tiles; ++i) {
-        const int tile = wg + i * G;
+        const int tile_next = tile_at(i + 1);
         const bool more = i + 1 < my_tiles;
         f32x4_t acc2[SUB] = {};
         static_for<0, C>([&](auto J) {
@@ -453,7 +454,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
           // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
           if (more) wait_vm<WL * (C - 1)>(); else wait_vm<WL * (C - 1 - j)>();
           unit(ring[kw] + WS * j, J, false, acc2, [&] {
-            if (more) issue(tile + G, j, ring[kw] + WS * j, false);
+            if (more) issue(tile_next, j, ring[kw] + WS * j, false);
           });
         });
         if (!park(acc2, more)) break;
@@ -462,7 +463,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   } else {
     // x travels with every unit: D units in flight in D slots of SLOT.
     for (int i = 0; i < my_tiles; ++i) {
-      const int tile = wg + i * G;
+      const int tile = tile_at(i), tile_next = tile_at(i + 1);
       const bool more = i + 1 < my_tiles;
       f32x4_t acc[SUB] = {};
       static_for<0, C>([&](auto J) {
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
           if constexpr (j + D < C) {
             issue(tile, j + D, ring[kw] + slot * SLOT, true);
           } else {
-            if (more) issue(tile + G, j + D - C, ring[kw] + slot * SLOT, true);
+            if (more) issue(tile_next, j + D - C, ring[kw] + slot * SLOT, true);
           }
         });
       });

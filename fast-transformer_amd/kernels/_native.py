@@ -93,6 +93,7 @@ SIGNATURES = {
     "ftk_last_hip_error": (_int, []),
     "ftk_device_compute_units": (_int, []),
     "ftk_persistent_programs": (_int, [_int, _int]),
+    "ftk_ring_tile": (_int, [_int, _int, _int, _int]),
     "ftk_linear_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ftk_rms_norm_linear_bf16": (_int, [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                         _c_void_p]),

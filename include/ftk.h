@@ -134,6 +134,12 @@ int ftk_device_compute_units(void);    /* CUs of the current device, or -1 witho
  * persistent_programs). The planner sizes the STREAM, QUAD, STAGE and MFMA_STREAM grids with it.
  * 0 when tiles or units is not positive. Host only. */
 int ftk_persistent_programs(int tiles, int units);
+/* Tile that step `step` of RING workgroup `wg` computes in a grid of `grid` over `tiles` tiles
+ * (the workgroup runs steps 0 .. ceil((tiles - wg) / grid) - 1). In every full round of `grid`
+ * tiles the workgroups of one XCD (wg % 8) take one contiguous run; otherwise wg + step * grid.
+ * No counterpart in the reference (its persistent kernels take tile pid + i * programs); exported
+ * so the mapping can be checked on the host. -1 for a step the workgroup does not run. Host only. */
+int ftk_ring_tile(int wg, int step, int grid, int tiles);
 
 /* ---- projections ------------------------------------------------------------ */
 

@@ -63,6 +63,30 @@ def test_persistent_programs_in_the_library_known_answers():
             assert lib.ftk_persistent_programs(tiles, units) == helpers.persistent_programs(tiles, units)
 
 
+def test_ring_tile_mapping_covers_every_tile_once():
+    """The RING kernels' tile of each (workgroup, step) (csrc/ftk_plan.h ring_tile): every tile
+    exactly once; in a full round of a grid that is a multiple of 8, the workgroups of one XCD
+    (wg % 8) hold one contiguous run of grid / 8 tiles, in workgroup order; otherwise wg + step grid."""
+    lib = _native.lib()
+    for tiles, grid in ((1536, 256), (512, 256), (256, 256), (9496, 500), (1000, 256), (300, 192), (77, 40),
+                        (263, 256), (10, 3), (384, 192)):
+        seen = []
+        for wg in range(grid):
+            steps = (tiles - wg + grid - 1) // grid
+            for step in range(steps):
+                t = lib.ftk_ring_tile(wg, step, grid, tiles)
+                seen.append(t)
+                full = (step + 1) * grid <= tiles
+                if grid % 8 == 0 and full:
+                    per = grid // 8
+                    assert t == step * grid + per * (wg % 8) + wg // 8, (tiles, grid, wg, step)
+                else:
+                    assert t == wg + step * grid, (tiles, grid, wg, step)
+            assert lib.ftk_ring_tile(wg, steps, grid, tiles) == -1
+        assert sorted(seen) == list(range(tiles)), (tiles, grid)
+    assert lib.ftk_ring_tile(0, 0, 0, 10) == -1 and lib.ftk_ring_tile(5, 0, 4, 10) == -1
+
+
 def test_invalid_arguments_rejected_before_any_launch():
     lib = _native.lib()
     assert lib.ftk_linear_bf16(None, None, None, 1, 8, 8, None) == _native.FTK_ERR_INVALID
