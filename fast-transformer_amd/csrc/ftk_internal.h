@@ -133,9 +133,9 @@ hipError_t launch_stage(const ProjArgs& a, int epi, const StageShape& shape, hip
 struct RingShape {
   int depth;     // D: units (K segments of one tile) in flight per wave
   int kw;        // waves per workgroup, splitting K
-  int grid;      // workgroups; each walks tiles wg, wg + grid, ...
+  int grid;      // workgroups; workgroup wg takes tile ring_tile(wg, i, grid, tiles) at step i
   int tiles;
-  int rows;      // RT: weight rows per tile (16, or 24)
+  int rows;      // RT: weight rows per tile (12, 16 or 24)
 };
 bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows = 16);
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& shape, hipStream_t stream);

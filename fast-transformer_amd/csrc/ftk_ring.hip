@@ -16,11 +16,15 @@
 //
 // Layout and schedule:
 //   * A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows)
-//     over all of K, or 24 (two MFMA subtiles, the second half used) where 16-row
-//     tiles would leave a partial round of workgroups. A workgroup is KW waves splitting K; wave kw owns the
-//     128-wide K segments j KW + kw (j < C, K = 128 C KW). A unit is one segment
-//     of one tile: 4 KiB of weights (4 loads of 4 rows x 256 bytes) and, while
-//     the B operand is not held in registers, 4 NX rows of x (NX loads).
+//     over all of K, or 12 or 24 (one subtile with four pad rows, or two MFMA
+//     subtiles with the second half used) where 16-row tiles would leave a
+//     partial round of workgroups. A workgroup is KW waves splitting K; wave kw
+//     owns the 128-wide K segments j KW + kw (j < C, K = 128 C KW). A unit is one
+//     segment of one tile: RT / 4 KiB of weights (RT / 4 loads of 4 rows x 256
+//     bytes) and, while the B operand is not held in registers, 4 NX rows of x
+//     (NX loads).
+//   * Workgroup wg takes tile ring_tile(wg, i, G, tiles) at step i: in a full
+//     round the workgroups of one XCD take one contiguous run of tiles.
 //   * Lane l of load q brings row 4 q + l / 16, chunk (l % 16) ^ h(row), into
 //     slot row * 16 + l % 16 of the unit's LDS: the XOR-swizzled layout whose
 //     MFMA reads (lane l: row l % 16, chunk 4 s + l / 16) hit 16 distinct
