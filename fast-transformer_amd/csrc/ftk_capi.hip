@@ -391,6 +391,12 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // share; lm_head + argmax in two rounds.
     const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : (d.groups_per_cu ? d.groups_per_cu : 1)) * cus;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
+    // A grid that is a multiple of 8 lets ring_tile give each XCD one contiguous
+    // run of tiles per full round: round up to one (more workgroups never make a
+    // walk longer). lm_head + argmax at 5 / 8 / 16 rows: 504 workgroups instead
+    // of 500, 1-2 us faster per call on MI355X.
+    const int even = (p->grid + 7) / 8 * 8;
+    if (even <= p->tiles) p->grid = even;
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
     return FTK_OK;
   }
@@ -632,12 +638,14 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
     return FTK_OK;
   }
   if (p->kind == FTK_KIND_RING) {
-    // Workgroup b walks tiles b + i grid; unit rows 0..15 of a tile.
+    // Workgroup b takes tile ring_tile(b, i, grid, tiles) at step i (as the kernel
+    // does); unit rows 0..RT-1 of a tile.
     if (p->grid < 1 || p->grid > p->tiles) return FTK_ERR_INVALID;
     const int rt = p->rows_per_wave;
     const int per = ring_out_per_tile(epilogue, rt);
     for (int b = 0; b < p->grid; ++b)
-      for (int tile = b; tile < p->tiles; tile += p->grid) {
+      for (int i = 0; b + i * p->grid < p->tiles; ++i) {
+        const int tile = ring_tile(b, i, p->grid, p->tiles);
         for (int r = 0; r < rt; ++r) {
           const int64_t row = ring_weight_row(epilogue, tile, r, (int)N, rt);
           if (row > *max_row) *max_row = row;

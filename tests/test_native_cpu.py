@@ -68,7 +68,7 @@ def test_ring_tile_mapping_covers_every_tile_once():
     exactly once; in a full round of a grid that is a multiple of 8, the workgroups of one XCD
     (wg % 8) hold one contiguous run of grid / 8 tiles, in workgroup order; otherwise wg + step grid."""
     lib = _native.lib()
-    for tiles, grid in ((1536, 256), (512, 256), (256, 256), (9496, 500), (1000, 256), (300, 192), (77, 40),
+    for tiles, grid in ((1536, 256), (512, 256), (256, 256), (9496, 500), (9496, 504), (1000, 256), (300, 192), (77, 40),
                         (263, 256), (10, 3), (384, 192)):
         seen = []
         for wg in range(grid):
@@ -379,7 +379,7 @@ def test_plan_kinds():
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # 16 x rows: two units fit
     assert p.kind == _native.KIND_RING and p.unroll == 2
     _native.call("ftk_plan_project", 5, 151936, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_RING and p.tiles == 9496 and p.grid == 500  # lm_head: two rounds
+    assert p.kind == _native.KIND_RING and p.tiles == 9496 and p.grid == 504  # lm_head: two rounds, 8 | grid
     # the prologue's residual add is not a RING form: such calls plan as before
     _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, None, p)
     assert p.kind == _native.KIND_QUAD
