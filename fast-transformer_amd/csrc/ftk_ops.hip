@@ -112,6 +112,233 @@ __global__ __launch_bounds__(kThreads) void swiglu_kernel(const void* __restrict
   out[i] = (uint16_t)swiglu_bf16(g, u);
 }
 
+// ---- Row-resident forms ------------------------------------------------------
+// For rows of cols % 8 == 0 elements, at most 8 kThreads R of them, on 16-byte
+// aligned pointers. Thread t holds chunks t, t + kThreads, ... (8 elements each)
+// of its row in registers, so every load of a row goes out at once: one round
+// trip instead of one per loop step. The squares are summed through
+// sum_squares8 in that chunk order and the wave totals in wave order, as the
+// STREAM kind's prologue sums them (thread t: chunks t, t + 256, ...), so
+// rms_norm followed by an M = 1 projection scales each row exactly as the
+// fused default does at M = 1. The output pass reads nothing but registers
+// (the gain is loaded beside the row).
+// Loads are unconditional (a chunk index past the row re-reads the last chunk,
+// whose value is then replaced by zero), so no branch joins wait on them.
+
+// bf16(bf16(v * scale) * gain) for 8 values, as stored (every NaN as 0x7FC0):
+// the cast order of engine/kernels/rmsnorm.py:35-46.
+__device__ __forceinline__ u32x4_t norm8_store(u32x4_t v, u32x4_t g, float scale) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+  const uint32_t ge[4] = {g[0], g[1], g[2], g[3]};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t n = rne_pair(lo_f32(e[i]) * scale, hi_f32(e[i]) * scale);
+    o[i] = pack_bf16(lo_f32(n) * lo_f32(ge[i]), hi_f32(n) * hi_f32(ge[i]));
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// 4 FP32 values from a 16-byte chunk (elements copied to scalars first, as widen8 does).
+__device__ __forceinline__ void widen4f(u32x4_t v, float* out) {
+  const uint32_t e[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(e[i]);
+}
+
+// Chunk j of this thread, clamped into the row for an unconditional load.
+__device__ __forceinline__ int row_chunk(int j, int chunks) {
+  const int c = (int)threadIdx.x + j * kThreads;
+  return c < chunks ? c : chunks - 1;
+}
+__device__ __forceinline__ bool own_chunk(int j, int chunks) { return (int)threadIdx.x + j * kThreads < chunks; }
+
+// Sum of squares of R chunks (zero chunks add nothing) and the row's scale.
+template <int R>
+__device__ __forceinline__ float rows_scale(const u32x4_t (&v)[R], int cols, float eps, float* red) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) ss = sum_squares8(v[j], ss);
+  return 1.0f / sqrtf(block_sum(ss, red) / (float)cols + eps);
+}
+
+template <int R>
+__global__ __launch_bounds__(kThreads) void rms_norm_rows_kernel(const uint16_t* __restrict__ x, int64_t row_stride,
+                                                                 const uint16_t* __restrict__ gamma,
+                                                                 uint16_t* __restrict__ y, int cols, float eps) {
+  __shared__ float red[kWaves];
+  const int chunks = cols >> 3;
+  const uint16_t* xr = x + (int64_t)blockIdx.x * row_stride;
+  uint16_t* yr = y + (int64_t)blockIdx.x * cols;
+  u32x4_t v[R], g[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) v[j] = load16(xr + 8 * row_chunk(j, chunks));
+#pragma unroll
+  for (int j = 0; j < R; ++j) g[j] = load16(gamma + 8 * row_chunk(j, chunks));
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (!own_chunk(j, chunks)) v[j] = u32x4_t{0u, 0u, 0u, 0u};
+  const float scale = rows_scale(v, cols, eps, red);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (own_chunk(j, chunks)) store16(yr + 8 * ((int)threadIdx.x + j * kThreads), norm8_store(v[j], g[j], scale));
+}
+
+template <int R>
+__global__ __launch_bounds__(kThreads) void embed_rms_norm_rows_kernel(const void* __restrict__ ids, int ids_bytes,
+                                                                       const uint16_t* __restrict__ table,
+                                                                       const uint16_t* __restrict__ gamma,
+                                                                       uint16_t* __restrict__ y,
+                                                                       uint16_t* __restrict__ hidden, int cols,
+                                                                       float eps) {
+  __shared__ float red[kWaves];
+  const int chunks = cols >> 3;
+  const int r = blockIdx.x;
+  const int64_t id = ids_bytes == 8 ? reinterpret_cast<const int64_t*>(ids)[r]
+                                    : (int64_t) reinterpret_cast<const int32_t*>(ids)[r];
+  const uint16_t* xr = table + id * cols;
+  u32x4_t v[R], g[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) g[j] = load16(gamma + 8 * row_chunk(j, chunks));
+#pragma unroll
+  for (int j = 0; j < R; ++j) v[j] = load16(xr + 8 * row_chunk(j, chunks));
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (!own_chunk(j, chunks)) v[j] = u32x4_t{0u, 0u, 0u, 0u};
+  const float scale = rows_scale(v, cols, eps, red);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (own_chunk(j, chunks)) {
+      const int64_t at = (int64_t)r * cols + 8 * ((int)threadIdx.x + j * kThreads);
+      store16(hidden + at, v[j]);
+      store16(y + at, norm8_store(v[j], g[j], scale));
+    }
+}
+
+// S == 0: x is BF16. S = 1..4: x is S FP32 partial planes, summed in split
+// order and rounded once (engine/kernels/merged.py:37-45), then added to the
+// residual as a BF16 tensor operation (rmsnorm.py:86-88).
+template <int R, int S>
+__global__ __launch_bounds__(kThreads) void add_rms_norm_rows_kernel(const void* __restrict__ x, int64_t split_stride,
+                                                                     const uint16_t* __restrict__ residual,
+                                                                     const uint16_t* __restrict__ gamma,
+                                                                     uint16_t* __restrict__ y,
+                                                                     uint16_t* __restrict__ sum, int cols,
+                                                                     float eps) {
+  __shared__ float red[kWaves];
+  const int chunks = cols >> 3;
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  u32x4_t v[R], g[R], r[R];
+  if constexpr (S == 0) {
+    const uint16_t* xr = reinterpret_cast<const uint16_t*>(x) + base;
+#pragma unroll
+    for (int j = 0; j < R; ++j) v[j] = load16(xr + 8 * row_chunk(j, chunks));
+#pragma unroll
+    for (int j = 0; j < R; ++j) r[j] = load16(residual + base + 8 * row_chunk(j, chunks));
+#pragma unroll
+    for (int j = 0; j < R; ++j) g[j] = load16(gamma + 8 * row_chunk(j, chunks));
+#pragma unroll
+    for (int j = 0; j < R; ++j) v[j] = add8(v[j], r[j]);
+  } else {
+    const float* xr = reinterpret_cast<const float*>(x) + base;
+    u32x4_t p[S][R][2];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        const float* at = xr + s * split_stride + 8 * row_chunk(j, chunks);
+        p[s][j][0] = load16(at);
+        p[s][j][1] = load16(at + 4);
+      }
+#pragma unroll
+    for (int j = 0; j < R; ++j) r[j] = load16(residual + base + 8 * row_chunk(j, chunks));
+#pragma unroll
+    for (int j = 0; j < R; ++j) g[j] = load16(gamma + 8 * row_chunk(j, chunks));
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      float t[8];
+      widen4f(p[0][j][0], t);
+      widen4f(p[0][j][1], t + 4);
+#pragma unroll
+      for (int s = 1; s < S; ++s) {
+        float q[8];
+        widen4f(p[s][j][0], q);
+        widen4f(p[s][j][1], q + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] += q[e];
+      }
+      const uint32_t re[4] = {r[j][0], r[j][1], r[j][2], r[j][3]};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = pack_bf16(round_bf16(t[2 * i]) + lo_f32(re[i]), round_bf16(t[2 * i + 1]) + hi_f32(re[i]));
+      v[j] = u32x4_t{o[0], o[1], o[2], o[3]};
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (!own_chunk(j, chunks)) v[j] = u32x4_t{0u, 0u, 0u, 0u};
+  const float scale = rows_scale(v, cols, eps, red);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (own_chunk(j, chunks)) {
+      const int64_t at = base + 8 * ((int)threadIdx.x + j * kThreads);
+      store16(sum + at, v[j]);
+      store16(y + at, norm8_store(v[j], g[j], scale));
+    }
+}
+
+// SwiGLU on V outputs per thread (width % 8 == 0, 16-byte aligned), the gate and
+// up values loaded together: V = 8 from BF16 (two 16-byte loads), V = 4 from S
+// FP32 partial planes (two 16-byte loads per plane, so twice the threads).
+template <int S>
+__global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(const void* __restrict__ packed, int64_t split_stride,
+                                                               uint16_t* __restrict__ out, int width,
+                                                               int64_t groups) {
+  constexpr int V = S == 0 ? 8 : 4;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= groups) return;
+  const int64_t per_row = width / V;
+  const int64_t row = i / per_row, j = i - row * per_row;
+  const int64_t g_off = row * 2 * width + V * j;
+  float g[V], u[V];
+  if constexpr (S == 0) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(packed);
+    widen8(load16(p + g_off), g);
+    widen8(load16(p + g_off + width), u);
+  } else {
+    const float* p = reinterpret_cast<const float*>(packed);
+    u32x4_t q[S][2];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      q[s][0] = load16(p + s * split_stride + g_off);
+      q[s][1] = load16(p + s * split_stride + g_off + width);
+    }
+    widen4f(q[0][0], g);
+    widen4f(q[0][1], u);
+#pragma unroll
+    for (int s = 1; s < S; ++s) {
+      float a[4], b[4];
+      widen4f(q[s][0], a);
+      widen4f(q[s][1], b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        g[e] += a[e];
+        u[e] += b[e];
+      }
+    }
+  }
+  uint32_t o[V / 2];
+#pragma unroll
+  for (int k = 0; k < V / 2; ++k)
+    o[k] = swiglu_bf16(g[2 * k], u[2 * k]) | (swiglu_bf16(g[2 * k + 1], u[2 * k + 1]) << 16);
+  uint16_t* dst = out + row * width + V * j;
+  if constexpr (V == 8)
+    store16(dst, u32x4_t{o[0], o[1], o[2], o[3]});
+  else
+    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{o[0], o[1]};
+}
+
 // Stage one: one workgroup per (row, column block of 8192) reduces its block to
 // a key (orderable BF16 value, inverted index) and stores it (argmax.py:19-31).
 constexpr int kArgmaxBlock = 8192;
@@ -187,33 +414,89 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const float* __r
   out[i] = (uint16_t)f32_to_bf16(total);
 }
 
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// 16-byte chunks per thread of the row-resident forms for a row of `cols`
+// elements, or 0 where only the element loop applies (ragged or long rows).
+int rows_chunks(int64_t cols) {
+  if (cols % 8 != 0 || cols > 8 * kThreads * 4) return 0;
+  const int64_t per = (cols / 8 + kThreads - 1) / kThreads;
+  return per <= 1 ? 1 : per <= 2 ? 2 : 4;
+}
+
+}  // namespace
+
 hipError_t launch_rms_norm(const uint16_t* x, int64_t row_stride, const uint16_t* gamma, uint16_t* y, int rows,
                            int cols, float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, row_stride, gamma, y, cols, eps);
+  const int r = rows_chunks(cols);
+  if (r && row_stride % 8 == 0 && aligned16(x) && aligned16(gamma) && aligned16(y)) {
+    auto kernel = r == 1 ? rms_norm_rows_kernel<1> : r == 2 ? rms_norm_rows_kernel<2> : rms_norm_rows_kernel<4>;
+    hipLaunchKernelGGL(kernel, dim3(rows), dim3(kThreads), 0, stream, x, row_stride, gamma, y, cols, eps);
+  } else {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, row_stride, gamma, y, cols, eps);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_embed_rms_norm(const void* ids, int ids_bytes, const uint16_t* table, const uint16_t* gamma,
                                  uint16_t* y, uint16_t* hidden, int rows, int cols, float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(embed_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, ids, ids_bytes, table, gamma, y,
-                     hidden, cols, eps);
+  const int r = rows_chunks(cols);
+  if (r && aligned16(table) && aligned16(gamma) && aligned16(y) && aligned16(hidden)) {
+    auto kernel = r == 1   ? embed_rms_norm_rows_kernel<1>
+                  : r == 2 ? embed_rms_norm_rows_kernel<2>
+                           : embed_rms_norm_rows_kernel<4>;
+    hipLaunchKernelGGL(kernel, dim3(rows), dim3(kThreads), 0, stream, ids, ids_bytes, table, gamma, y, hidden, cols,
+                       eps);
+  } else {
+    hipLaunchKernelGGL(embed_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, ids, ids_bytes, table, gamma, y,
+                       hidden, cols, eps);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_add_rms_norm(const void* x, int splits, int64_t split_stride, const uint16_t* residual,
                                const uint16_t* gamma, uint16_t* y, uint16_t* sum, int rows, int cols, float eps,
                                hipStream_t stream) {
-  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, splits, split_stride, residual,
-                     gamma, y, sum, cols, eps);
+  const int r = rows_chunks(cols);
+  if (r && splits <= 4 && (splits == 0 || split_stride % 4 == 0) && aligned16(x) && aligned16(residual) &&
+      aligned16(gamma) && aligned16(y) && aligned16(sum)) {
+    typedef void (*Kernel)(const void*, int64_t, const uint16_t*, const uint16_t*, uint16_t*, uint16_t*, int, float);
+    static const Kernel table[3][5] = {
+        {add_rms_norm_rows_kernel<1, 0>, add_rms_norm_rows_kernel<1, 1>, add_rms_norm_rows_kernel<1, 2>,
+         add_rms_norm_rows_kernel<1, 3>, add_rms_norm_rows_kernel<1, 4>},
+        {add_rms_norm_rows_kernel<2, 0>, add_rms_norm_rows_kernel<2, 1>, add_rms_norm_rows_kernel<2, 2>,
+         add_rms_norm_rows_kernel<2, 3>, add_rms_norm_rows_kernel<2, 4>},
+        {add_rms_norm_rows_kernel<4, 0>, add_rms_norm_rows_kernel<4, 1>, add_rms_norm_rows_kernel<4, 2>,
+         add_rms_norm_rows_kernel<4, 3>, add_rms_norm_rows_kernel<4, 4>},
+    };
+    hipLaunchKernelGGL(table[r == 1 ? 0 : r == 2 ? 1 : 2][splits], dim3(rows), dim3(kThreads), 0, stream, x,
+                       split_stride, residual, gamma, y, sum, cols, eps);
+  } else {
+    hipLaunchKernelGGL(add_rms_norm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, splits, split_stride, residual,
+                       gamma, y, sum, cols, eps);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const void* packed, int splits, int64_t split_stride, uint16_t* out, int rows, int width,
                          hipStream_t stream) {
   const int64_t total = (int64_t)rows * width;
-  const int64_t grid = (total + kThreads - 1) / kThreads;
-  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, packed, splits, split_stride,
-                     out, width, total);
+  if (width % 8 == 0 && splits <= 4 && (splits == 0 || split_stride % 4 == 0) && aligned16(packed) &&
+      aligned16(out)) {
+    typedef void (*Kernel)(const void*, int64_t, uint16_t*, int, int64_t);
+    static const Kernel table[5] = {swiglu_rows_kernel<0>, swiglu_rows_kernel<1>, swiglu_rows_kernel<2>,
+                                    swiglu_rows_kernel<3>, swiglu_rows_kernel<4>};
+    const int64_t groups = total / (splits == 0 ? 8 : 4);
+    const int64_t grid = (groups + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(table[splits], dim3((unsigned)grid), dim3(kThreads), 0, stream, packed, split_stride, out,
+                       width, groups);
+  } else {
+    const int64_t grid = (total + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, packed, splits, split_stride,
+                       out, width, total);
+  }
   return hipGetLastError();
 }
 

@@ -24,7 +24,10 @@ def swiglu(packed):
     output = torch.empty((*shape[:-1], width), device=data.device, dtype=torch.bfloat16)
     rows = output.numel() // width
     data = data.contiguous()
-    _native.call("ftk_swiglu_bf16", _native.ptr(data), 0 if splits == 1 else splits, count if splits > 1 else 0,
+    # FP32 data is a Split's partials, one plane included (summed and rounded once);
+    # BF16 data is read as stored.
+    partials = data.dtype == torch.float32
+    _native.call("ftk_swiglu_bf16", _native.ptr(data), splits if partials else 0, count if partials else 0,
                  _native.ptr(output), rows, width, _native.stream_of(data))
     return output
 
