@@ -31,6 +31,8 @@ def argmax(logits, block=8192, top=None):
     vocab = logits.shape[-1]
     rows = logits.numel() // vocab
     out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=logits.device)
+    if rows == 0:
+        return out
     ws = _native.argmax_workspace(logits.device, rows, vocab)
     if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < rows):
         raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
@@ -64,6 +66,8 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
     out = torch.empty((*shape[:-1], v), dtype=torch.bfloat16, device=x.device) if logits else None
     if top is not None and (top.dtype != torch.float32 or not top.is_contiguous() or top.numel() < m):
         raise ValueError("top must be a contiguous FP32 tensor with one slot per row")
+    if m == 0:
+        return ids, out
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
     if config is None and residual is None and _fusable(flat, weight, norm_weight):
         # selected like a plain projection, under its own key (kernels/linear.py _choice); the

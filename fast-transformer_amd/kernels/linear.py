@@ -119,6 +119,8 @@ def project(x, weight, config=None, out=None):
         raise ValueError(f"x has K={k}, weight has K={weight.shape[1]}")
     if out is None:
         out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    if m == 0:
+        return out
     status = fused_project(x, weight, _native.EPI_STORE, out, config=config)
     if status == _native.FTK_ERR_UNSUPPORTED:
         if config is not None:
@@ -143,6 +145,8 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
     flat = _as_rows(x)
     m, k = flat.shape
     n = weight.shape[0]
+    if m == 0:
+        return torch.empty((*shape[:-1], n), device=x.device, dtype=torch.bfloat16)
 
     def fused(cfg, w, inp=flat):
         y = torch.empty((inp.shape[0], w.shape[0]), device=inp.device, dtype=torch.bfloat16)
@@ -177,6 +181,8 @@ def add_rms_norm_linear(x, residual, norm_weight, eps, weight, config=None):
     n = weight.shape[0]
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
     summed = torch.empty_like(res)
+    if m == 0:
+        return out.reshape(*shape[:-1], n), summed.reshape(shape)
     status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
         fused_project(flat, weight, _native.EPI_STORE, out, norm_weight, eps, residual=res, summed=summed,
                       config=config)
@@ -200,6 +206,8 @@ def embed_rms_norm_linear(token_ids, table, norm_weight, eps, weight, config=Non
     n = weight.shape[0]
     out = torch.empty((ids.numel(), n), device=table.device, dtype=torch.bfloat16)
     hidden = torch.empty((ids.numel(), k), device=table.device, dtype=torch.bfloat16)
+    if ids.numel() == 0:
+        return out.reshape(*token_ids.shape, n), hidden.reshape(*token_ids.shape, k)
     status = _native.FTK_ERR_UNSUPPORTED if prefer_native(ids.numel(), config) else \
         fused_project(table.contiguous(), weight, _native.EPI_STORE, out, norm_weight, eps, x_ids=ids,
                       summed=hidden, config=config)
@@ -433,6 +441,8 @@ def linear_residual(x, weight, residual, config=None):
     res = residual.reshape(-1, n).contiguous()
     m = flat.shape[0]
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    if m == 0:
+        return out.reshape(*x.shape[:-1], n)
     cfg = ctypes.byref(config) if config is not None else None
     _native.call("ftk_project_add_bf16", _native.ptr(flat), _native.ptr(weight), _native.ptr(res), _native.ptr(out),
                  m, n, k, cfg, _native.stream_of(flat))
@@ -450,6 +460,8 @@ def linear(x, weight, split_ok=False):
     if rows > MAX_ROWS or x.dtype != torch.bfloat16 or not weight.is_contiguous():
         return F.linear(x, weight)
     _native.require_gpu(x, weight)
+    if rows == 0:
+        return x.new_empty((*x.shape[:-1], weight.shape[0]))
     flat = _as_rows(x)
 
     def run(choice, w, inp=flat):

@@ -30,6 +30,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     if weight.numel() != n_cols:
         raise ValueError(f"norm weight has {weight.numel()} elements for {n_cols} columns")
     out = torch.empty_like(rows)
+    if n_rows == 0:
+        return out.reshape(shape)
     _native.call("ftk_rms_norm_bf16", _native.ptr(rows), rows.stride(0), _native.ptr(weight.contiguous()),
                  _native.ptr(out), n_rows, n_cols, float(eps), _native.stream_of(rows))
     return out.reshape(shape)
@@ -52,6 +54,8 @@ def add_rms_norm(x, residual, weight, eps):
     out = torch.empty_like(residual_rows)
     summed = torch.empty_like(residual_rows)
     rows = residual_rows.shape[0]
+    if rows == 0:
+        return out.reshape(shape), summed.reshape(shape)
     # splits == 1 is a BF16 tensor (C ABI: 0 splits); otherwise FP32 partials [S, rows * width].
     _native.call("ftk_add_rms_norm_bf16", _native.ptr(x_rows), 0 if splits == 1 else splits,
                  count if splits > 1 else 0, _native.ptr(residual_rows), _native.ptr(weight.contiguous()),
@@ -72,7 +76,9 @@ def embed_rms_norm(token_ids, table, weight, eps):
     n_cols = table.shape[1]
     hidden = torch.empty((ids.numel(), n_cols), dtype=table.dtype, device=table.device)
     out = torch.empty_like(hidden)
+    shape = (*token_ids.shape, n_cols)
+    if ids.numel() == 0:
+        return out.reshape(shape), hidden.reshape(shape)
     _native.call("ftk_embed_rms_norm_bf16", _native.ptr(ids), 8, _native.ptr(table), _native.ptr(weight.contiguous()),
                  _native.ptr(out), _native.ptr(hidden), ids.numel(), n_cols, float(eps), _native.stream_of(table))
-    shape = (*token_ids.shape, n_cols)
     return out.reshape(shape), hidden.reshape(shape)

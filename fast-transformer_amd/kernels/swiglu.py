@@ -23,6 +23,8 @@ def swiglu(packed):
     width = shape[-1] // 2
     output = torch.empty((*shape[:-1], width), device=data.device, dtype=torch.bfloat16)
     rows = output.numel() // width
+    if rows == 0:
+        return output
     data = data.contiguous()
     # FP32 data is a Split's partials, one plane included (summed and rounded once);
     # BF16 data is read as stored.
@@ -56,6 +58,9 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
     out = torch.empty((m, n // 2), device=x.device, dtype=torch.bfloat16)
     res = None if residual is None else residual.reshape(-1, shape[-1]).contiguous()
     summed = None if residual is None else torch.empty_like(res)
+    if m == 0:
+        act = out.reshape(*shape[:-1], n // 2)
+        return act if residual is None else (act, summed.reshape(shape))
     if config is None and residual is None and _fusable(flat, gate_up_weight, norm_weight):
         # selected like a plain projection, under its own key (kernels/linear.py _choice)
         def run(choice, w, inp=flat):
