@@ -597,6 +597,8 @@ def shapes_table(model8, step8, dev):
         flops = 2 * m * sum(n * k for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)))
         out[f"C4 8B layer M={m}"] = shape_entry(us, byts, flops)
         stage(f"C4 M={m} done")
+    out.update(vendor_table(model8, dev))
+    stage("C4 projections against hipBLASLt done")
     # C3 per layer (M=1)
     g = capture(step8.layers)
     us = time_graph(g, reps=5) / cfg["layers"]
@@ -626,6 +628,29 @@ def shapes_table(model8, step8, dev):
     us = time_graph(g) / 64
     out["C1 0.6B qkv M=1 (no prologue)"] = shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096)
     del model06, copies
+    return out
+
+
+def vendor_table(model8, dev):
+    """Each C4 weight shape as a plain projection (no norm, no SwiGLU) at M = 5, 8, 16: this library's
+    planner default against torch's native GEMM (hipBLASLt), each a graph over the 36 layers' distinct
+    weights, same process. µs per launch; the entry's figures are this library's."""
+    out = {}
+    cfg = model8.cfg
+    for m in (5, 8, 16):
+        gen = torch.Generator(device=dev).manual_seed(100 + m)
+        for kind in ("qkv", "o", "gate_up", "down"):
+            k = cfg["inter"] if kind == "down" else cfg["hidden"]
+            x = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+            ws = [lw[kind] for lw in model8.layers]
+            ys = [torch.empty((m, w.shape[0]), device=dev, dtype=torch.bfloat16) for w in ws]
+            ours = time_graph(capture(lambda: [L.project(x, w, out=y) for w, y in zip(ws, ys)]), reps=5) / len(ws)
+            native = time_graph(capture(lambda: [torch.nn.functional.linear(x, w) for w in ws]), reps=5) / len(ws)
+            n = ws[0].shape[0]
+            e = shape_entry(ours, 2 * n * k + 2 * m * k + 2 * m * n, 2 * m * n * k)
+            e["hipblaslt_us"] = round(native, 3)
+            e["speedup_vs_hipblaslt"] = round(native / ours, 3)
+            out[f"C4 8B {kind} GEMM M={m} vs hipBLASLt"] = e
     return out
 
 
