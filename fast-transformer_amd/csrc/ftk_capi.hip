@@ -94,9 +94,14 @@ static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
 // several tiles (the prologue is paid once per workgroup), mid-size ones one
 // tile per workgroup, the largest (lm_head) as deep walks of kStreamMaxTiles.
 // Rows of at most 1024 elements (Qwen3-0.6B's QKV and gate/up) take two tiles
-// per workgroup (0.6B gate/up + SwiGLU: 4.70 -> 4.45 us).
-static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K) {
-  if (K <= 1024 && tiles <= 4096) return tiles / 2 > 2LL * cus ? tiles / 2 : 2LL * cus;
+// per workgroup when a prologue is paid per workgroup (0.6B gate/up + SwiGLU:
+// 4.70 -> 4.45 us), one without it (0.6B QKV without the norm: 3.60 -> 3.48 us,
+// graphs of 64 distinct weights).
+static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K, bool pro) {
+  if (K <= 1024 && tiles <= 4096) {
+    if (!pro) return tiles;
+    return tiles / 2 > 2LL * cus ? tiles / 2 : 2LL * cus;
+  }
   // Long rows (down, K = 12288): at M = 1 one tile per workgroup; with more x
   // rows one workgroup per CU walking tiles (M = 2..4: 16.9-17.9 us, against
   // 19.6-22.1 with one tile each).
@@ -323,7 +328,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // Fewest workgroups that keep every walk at the same depth, and no deeper than
     // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
-                                                  : stream_default_cap(p->tiles, cus, M, K);
+                                                  : stream_default_cap(p->tiles, cus, M, K, pro);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
