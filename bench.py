@@ -208,7 +208,8 @@ def time_graph(graph, reps=10, inner=1, warm_s=0.0):
 def selection_summary():
     """The frozen launch choice of every shape the run selected (kernels/linear.py _CHOICES)."""
     names = {_native.KIND_GEMV: "gemv", _native.KIND_MFMA: "mfma", _native.KIND_STREAM: "stream",
-             _native.KIND_MFMA_STREAM: "mfma_stream", _native.KIND_QUAD: "quad", _native.KIND_STAGE: "stage"}
+             _native.KIND_MFMA_STREAM: "mfma_stream", _native.KIND_QUAD: "quad", _native.KIND_STAGE: "stage",
+             _native.KIND_RING: "ring"}
     out = {}
     for key, choice in L._CHOICES.items():
         op, rest = (key[0], key[2:]) if isinstance(key[0], str) else ("linear", key[1:])
@@ -219,7 +220,13 @@ def selection_summary():
             out[label] = "native (hipBLASLt via F.linear)"
         else:
             out[label] = names.get(choice[0], str(choice[0])) + str(list(choice[1:]))
-    return {"tuned": L.TUNE, "choices": out}
+    past = {}
+    for key, choice in L.inherited.items():
+        op, rest = (key[0], key[2:]) if isinstance(key[0], str) else ("linear", key[1:])
+        past[f"{op} M={rest[0]} N={rest[1]} K={rest[2]}"] = "untuned default" if choice in (None, "native") \
+            else "inherited " + names.get(choice[0], str(choice[0])) + str(list(choice[1:]))
+    return {"tuned": L.TUNE, "tuning_s": round(L.tuning_seconds, 1), "budget_s": L.PROCESS_SECONDS,
+            "past_budget": past, "choices": out}
 
 
 def shape_entry(us, byts, flops=None):

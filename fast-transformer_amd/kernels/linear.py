@@ -50,7 +50,7 @@ TUNE = os.environ.get("FTK_TUNE", "0") == "1"
 #: From this many rows the planner's default is torch's native GEMM (hipBLASLt), as the reference
 #: keeps cuBLAS unless a timed kind beats it (linear.py:455-475). Measured on MI355X at Qwen3-8B
 #: shapes: at 32 rows hipBLASLt is 1.6-2.7x faster than these kernels; at 16 and fewer rows these
-#: kernels are faster (1.03-2.2x) on every projection but down (K = 12288) at 16 rows.
+#: kernels are faster on every projection (1.09x for down at 16 rows, up to 2.1x for O).
 NATIVE_FROM_ROWS = 17
 
 
@@ -229,8 +229,16 @@ def embed_rms_norm_linear(token_ids, table, norm_weight, eps, weight, config=Non
 # this library's norm / SwiGLU / argmax kernels around it. The fused forms are selected the same
 # way as plain projections, each under its own key.
 
-#: Selection budget per shape, as the reference's _SHAPE_SECONDS (linear.py:347-348).
+#: Selection budgets per shape and per process, as the reference's _SHAPE_SECONDS and
+#: _PROCESS_SECONDS (linear.py:345-348). Past the process budget a shape is not timed: a verify
+#: block (5..MAX_ROWS rows) takes a choice already validated for the same weight at another row
+#: count (_inherit), any other shape its untuned default. FTK_TUNE_SECONDS sets the process budget.
 SHAPE_SECONDS = 6.0
+PROCESS_SECONDS = float(os.environ.get("FTK_TUNE_SECONDS", "28"))
+_TUNING_DEADLINE = None
+#: Seconds this process has spent timing candidates, and the shapes past the budget.
+tuning_seconds = 0.0
+inherited = {}
 #: Weight bytes cycled through per timing graph: distinct copies, so no call is served from the
 #: 256 MB MALL (the MI355X counterpart of _cold_graph_time's 128 MiB flush, linear.py:317-337).
 COLD_BYTES = 768 << 20
@@ -323,9 +331,15 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     weight ``w``; ``native(w)`` is the native-GEMM form. Every candidate must agree with the
     planner default on a fixed probe input before it is timed.
     """
+    global _TUNING_DEADLINE, tuning_seconds
     m, k = x.shape
     n = weight.shape[0]
     key = _key(op, x.device, m, n, k)
+    started = time.monotonic()
+    if _TUNING_DEADLINE is None:
+        _TUNING_DEADLINE = started + PROCESS_SECONDS
+    if started >= _TUNING_DEADLINE:
+        return _inherit(op, x, weight, run)
     copies = max(2, min(16, -(-COLD_BYTES // max(1, weight.numel() * weight.element_size()))))
     weights = [weight] + [weight.clone() for _ in range(copies - 1)]
     generator = torch.Generator(device=x.device).manual_seed(1729)
@@ -334,7 +348,7 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     if reference is None:
         return "native"
     reference = reference.clone()
-    deadline = time.monotonic() + SHAPE_SECONDS
+    deadline = min(_TUNING_DEADLINE, time.monotonic() + SHAPE_SECONDS)
     native_us = _cold_us(native, weights)
     best_us, best = native_us, "native"
     validated = [(native_us, "native")]
@@ -364,7 +378,47 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     validated.sort(key=lambda item: item[0])
     _VALIDATED[key] = validated
     del weights
+    tuning_seconds += time.monotonic() - started
     return best
+
+
+def _inherit(op, x, weight, run):
+    """The choice of a shape past the process budget (linear.py:412-433).
+
+    A verify block (5..MAX_ROWS rows) takes a launch choice already frozen for the same operation
+    and weight shape at another row count above 4, if it agrees with the planner default on a probe
+    input (the launch must also exist at this row count). Otherwise, and for other row counts, the
+    shape takes its untuned default. The captured step's ``refine`` still re-judges the choice.
+    """
+    m, k = x.shape
+    n = weight.shape[0]
+    key = _key(op, x.device, m, n, k)
+    default = "native" if prefer_native(m) else None
+    inherited[key] = default
+    _VALIDATED[key] = [(0.0, default)]
+    if m <= 4 or m > MAX_ROWS:
+        return default
+    generator = torch.Generator(device=x.device).manual_seed(1729)
+    probe = torch.randn(x.shape, device=x.device, dtype=x.dtype, generator=generator)
+    reference = run(None, weight, probe)
+    if reference is None:
+        return default
+    reference = reference.clone()
+    for other, choice in list(_CHOICES.items()):
+        if choice in (None, "native") or _key(op, x.device, other[-3], n, k) != other:
+            continue  # a default, or another operation, device or weight shape
+        if other[-3] <= 4:
+            continue
+        try:
+            got = run(choice, weight, probe)
+        except _native.FtkError:
+            continue  # the launch does not exist at this row count
+        if got is None or not _agrees(got, reference):
+            continue
+        _VALIDATED[key] = [(0.0, choice), (1.0, default)]
+        inherited[key] = choice
+        return choice
+    return default
 
 
 def _choice(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=False):

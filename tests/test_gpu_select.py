@@ -39,6 +39,8 @@ def tuning(monkeypatch):
     monkeypatch.setattr(L, "SHAPE_SECONDS", 2.0)
     monkeypatch.setattr(L, "_CHOICES", {})
     monkeypatch.setattr(L, "_VALIDATED", {})
+    monkeypatch.setattr(L, "_TUNING_DEADLINE", None)
+    monkeypatch.setattr(L, "inherited", {})
     monkeypatch.setattr(tune, "_REGISTRY", {})
     yield
 
@@ -142,3 +144,23 @@ def test_refine_keeps_a_graph_identical_to_eager(cuda, tuning):
         torch.cuda.synchronize()
         for got, want in zip(outs, eager):
             np.testing.assert_array_equal(to_bits(got), want)
+
+
+def test_past_the_process_budget_a_verify_block_inherits(cuda, tuning, monkeypatch):
+    """Past the process budget (linear.py:441-443) a 5..32-row shape takes a launch choice frozen for
+    the same weight at another row count above 4 once it agrees with the planner default
+    (_inherit, linear.py:412-433); a shape of 4 or fewer rows takes its untuned default."""
+    w = seeded((4096, 4096), 41, scale=0.02, device=cuda)
+    ring = (_native.KIND_RING, 16, 2, 1, 8)
+    L._CHOICES[(cuda, 8, 4096, 4096)] = ring  # as if selected at 8 rows before the budget ran out
+    monkeypatch.setattr(L, "_TUNING_DEADLINE", 0.0)
+    x5 = seeded((5, 4096), 42, device=cuda)
+    y5 = L.linear(x5, w)
+    assert L._CHOICES[(cuda, 5, 4096, 4096)] == ring
+    assert L.inherited[(cuda, 5, 4096, 4096)] == ring
+    assert _knob((cuda, 5, 4096, 4096)).get() == ring
+    assert within(to_bits(y5), path.project(to_bits(x5), to_bits(w)))
+    x3 = seeded((3, 4096), 43, device=cuda)
+    y3 = L.linear(x3, w)
+    assert L._CHOICES[(cuda, 3, 4096, 4096)] is None and L.inherited[(cuda, 3, 4096, 4096)] is None
+    assert within(to_bits(y3), path.project(to_bits(x3), to_bits(w)))
