@@ -368,6 +368,35 @@ __global__ __launch_bounds__(kThreads) void argmax_block_kernel(const uint16_t* 
   if (threadIdx.x == 0) keys[(size_t)blockIdx.x * rows + row] = best;  // [slot][row]
 }
 
+// Stage one for rows of vocab % 8 == 0 on 16-byte aligned logits: each thread
+// loads its four 8-logit chunks of the block (t, t + 256, ...) at once, so the
+// block costs one round trip. Same keys as argmax_block_kernel.
+__global__ __launch_bounds__(kThreads) void argmax_block_rows_kernel(const uint16_t* __restrict__ logits, int vocab,
+                                                                     unsigned long long* __restrict__ keys,
+                                                                     int rows) {
+  constexpr int kChunks = kArgmaxBlock / 8 / kThreads;  // 16-byte chunks per thread
+  __shared__ unsigned long long red[kWaves];
+  const int row = blockIdx.y;
+  const int begin = blockIdx.x * kArgmaxBlock;
+  const int n = (min(begin + kArgmaxBlock, vocab) - begin) >> 3;  // chunks in this block
+  const uint16_t* lr = logits + (int64_t)row * vocab + begin;
+  u32x4_t v[kChunks];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) v[j] = load16(lr + 8 * row_chunk(j, n));
+  unsigned long long best = 0ull;
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    if (!own_chunk(j, n)) continue;
+    const int c0 = begin + 8 * ((int)threadIdx.x + j * kThreads);
+    float f[8];
+    widen8(v[j], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) best = key_max(best, argmax_key(f[e], (uint32_t)(c0 + e)));
+  }
+  best = block_max_key(best, red);
+  if (threadIdx.x == 0) keys[(size_t)blockIdx.x * rows + row] = best;  // [slot][row]
+}
+
 // Stage two: one workgroup per row picks the best of ``slots`` keys and writes
 // the id (and the winning logit) (argmax.py:34-48 _first_best). The keys were
 // just written by other CUs, so every load is a long trip: each thread issues
@@ -503,7 +532,12 @@ hipError_t launch_swiglu(const void* packed, int splits, int64_t split_stride, u
 hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids, int ids_bytes, float* top,
                          unsigned long long* keys, hipStream_t stream) {
   const int blocks = argmax_blocks(vocab);
-  hipLaunchKernelGGL(argmax_block_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, keys, rows);
+  if (vocab % 8 == 0 && aligned16(logits))
+    hipLaunchKernelGGL(argmax_block_rows_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, keys,
+                       rows);
+  else
+    hipLaunchKernelGGL(argmax_block_kernel, dim3(blocks, rows), dim3(kThreads), 0, stream, logits, vocab, keys,
+                       rows);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_argmax_finalize(keys, blocks, rows, ids, ids_bytes, top, stream);

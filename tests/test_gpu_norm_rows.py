@@ -1,4 +1,4 @@
-"""GPU parity of the standalone norm and SwiGLU operators in both of their launch forms.
+"""GPU parity of the standalone norm, SwiGLU and argmax operators in both of their launch forms.
 
 Rows of a multiple of 8 elements, at most 8192, on 16-byte aligned buffers run the
 row-resident kernels (the whole row in registers, one round trip); other rows run the
@@ -16,6 +16,7 @@ from conftest import seeded, to_bits
 from oracle import path
 
 from kernels import _native
+from kernels import argmax as A
 from kernels import linear as L
 from kernels import merged as M
 from kernels import rmsnorm as R
@@ -148,3 +149,25 @@ def test_swiglu_forms(cuda, splits, rows, width):
         inputs = to_bits(merged)
     # SiLU's exp on the GPU is not correctly rounded: the oracle's bits on >= 99.9 %, 1 ulp at most.
     assert close(to_bits(got), path.swiglu(inputs), max_ulps=1)
+
+
+@pytest.mark.parametrize("rows,vocab", [(1, 151936), (5, 151936), (3, 8200), (2, 1000)])
+def test_argmax_both_forms(cuda, rows, vocab):
+    """The 16-byte-load block stage (vocab % 8 == 0, aligned logits) and the element loop give the
+    same ids and top logits, ties to the lowest index and NaN as the maximum included
+    (engine/kernels/argmax.py:19-48)."""
+    logits = seeded((rows, vocab), seed=vocab + rows, scale=3, device=cuda)
+    logits[0, vocab // 3] = logits[0, vocab // 2] = 40.0  # a tie: the lower index wins
+    if rows > 1:
+        logits[1, vocab - 1] = float("nan")
+    top_a, top_b = (torch.empty(rows, dtype=torch.float32, device=cuda) for _ in range(2))
+    fast = A.argmax(logits, top=top_a)
+    slow = A.argmax(misaligned(logits), top=top_b)
+    assert torch.equal(fast, slow)
+    assert torch.equal(top_a, top_b) or (torch.isnan(top_a) == torch.isnan(top_b)).all()
+    assert fast[0].item() == vocab // 3
+    if rows > 1:
+        assert fast[1].item() == vocab - 1
+    want = logits.float().argmax(-1)
+    for r in range(2 if rows > 1 else 1, rows):
+        assert fast[r].item() == want[r].item()
