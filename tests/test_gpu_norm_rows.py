@@ -171,3 +171,18 @@ def test_argmax_both_forms(cuda, rows, vocab):
     want = logits.float().argmax(-1)
     for r in range(2 if rows > 1 else 1, rows):
         assert fast[r].item() == want[r].item()
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 9, 17])
+@pytest.mark.parametrize("shape", [(1, 4096), (16, 24576), (3, 1000), (2, 999)])
+def test_merge_splits_any_planes(cuda, splits, shape):
+    """bf16(sum of the planes in split order), as the oracle sums them, for 1..17 planes, ragged
+    counts and partials that start off a 16-byte boundary."""
+    gen = torch.Generator(device=cuda).manual_seed(splits * 7 + shape[1])
+    partial = torch.randn((splits, *shape), generator=gen, device=cuda) * 50
+    want = path.merge_splits(partial.cpu().numpy())
+    assert np.array_equal(to_bits(M.materialize(M.Split(partial, shape))), want)
+    buf = torch.empty(partial.numel() + 1, device=cuda)
+    odd = buf[1:].view(partial.shape)
+    odd.copy_(partial)
+    assert np.array_equal(to_bits(M.materialize(M.Split(odd, shape))), want)
