@@ -362,6 +362,11 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
+    # rows of <= 1024 elements: one tile per workgroup without the norm (C1), two with it (C2)
+    _native.call("ftk_plan_project", 1, 4096, 1024, 0, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.grid == p.tiles == 1024
+    _native.call("ftk_plan_project", 1, 4096, 1024, _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.grid == 512 and p.tiles == 1024
     # 5..16 rows: weight and x segments loaded straight into LDS (RING), one workgroup per CU
     _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
     assert p.kind == _native.KIND_RING and p.threads == 512 and p.unroll == 2 and p.grid == 256
