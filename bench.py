@@ -435,7 +435,7 @@ def main():
                     help="profiling mode: PASSES eager passes of decode attention, then of rope_attend, over each "
                          "ATTN_CASES cache set (distinct caches), then one 1 GiB device copy as the counter reference")
     ap.add_argument("--profile-rows", type=str, default="", metavar="M[,M...]",
-                    help="profiling mode: two eager passes of the 36-layer projection chain at each M rows "
+                    help="profiling mode: two eager passes of the 36-layer projection set at each M rows "
                          "(the C4 workload), then one 1 GiB device copy as the counter reference")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -550,7 +550,7 @@ def profile_gate_up(cfg, dev, passes):
 
 
 def profile_rows(cfg, dev, rows):
-    """Eager passes of the 36-layer projection chain at M rows (for rocprofv3 counter runs), plus a
+    """Eager passes of the 36-layer projection set at M rows (for rocprofv3 counter runs), plus a
     copy of known size. Each layer is RMSNorm-prologue QKV, O, RMSNorm-prologue gate/up + SwiGLU, down."""
     model = Model(cfg, dev, head=False)
     for m in rows:
@@ -619,15 +619,12 @@ def shapes_table(model8, step8, dev):
     out["C3 8B layer M=1, residual add in the O / down epilogues"] = shape_entry(
         us, sum(lb.values()) + 4 * 2 * cfg["hidden"])
     del g
-    out.update(chain_entry("C3 8B layer M=1, all 36 layers in one chain launch", step8, sum(lb.values())))
     # C1 / C2: Qwen3-0.6B shapes
     model06 = Model(QWEN3_06B, dev, head=False, seed=2)
     st06 = Step(model06, 1, dev, seed=3)
     g = capture(st06.layers)
     us = time_graph(g, reps=10) / QWEN3_06B["layers"]
     out["C2 0.6B layer M=1"] = shape_entry(us, sum(layer_bytes(QWEN3_06B, 1).values()))
-    out.update(chain_entry("C2 0.6B layer M=1, all 28 layers in one chain launch", st06,
-                           sum(layer_bytes(QWEN3_06B, 1).values())))
     x = torch.randn((1, 1024), device=dev).to(torch.bfloat16)
     copies = [torch.randn((4096, 1024), device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(64)]
     ys = [torch.empty((1, 4096), device=dev, dtype=torch.bfloat16) for _ in range(64)]
@@ -659,26 +656,6 @@ def vendor_table(model8, dev):
             e["speedup_vs_hipblaslt"] = round(native / ours, 3)
             out[f"C4 8B {kind} GEMM M={m} vs hipBLASLt"] = e
     return out
-
-
-def chain_entry(label, step, layer_bytes_):
-    """The same M=1 projection set as ``Step.layers`` run as one projection chain (kernels/chain.py): one
-    cooperative launch for every layer, O fenced behind its layer's QKV as attention would be. µs per
-    layer over graph replays, plus each stage's median share from the kernel's own clock stamps."""
-    from kernels import chain as CH
-
-    n = len(step.model.layers)
-    chain, _ = CH.decode_layers(step.model.layers, step.h, step.attn, EPS, outputs="qkv")
-    chain.prepare()
-    chain.launch()
-    chain.status()
-    g = capture(chain.launch, warm=0)
-    us = time_graph(g, reps=10) / n
-    chain.status()
-    st = chain.stage_us()
-    stages = {name: round(statistics.median(st[k::4]), 2) for k, name in enumerate(("qkv", "o", "gate_up", "down"))}
-    del g, chain
-    return {label: {**shape_entry(us, layer_bytes_), "stage_us": stages}}
 
 
 #: Decode attention next to the projections (Qwen3-8B heads: 32 query, 8 KV, D = 128):

@@ -54,21 +54,6 @@ class Rows(ctypes.Structure):
                 ("x_rows", _i64)]
 
 
-class ChainStage(ctypes.Structure):
-    """ftk_chain_stage: one projection of a chain (-1 = no source / residual source / fence)."""
-
-    _fields_ = [("w", _c_void_p), ("gamma", _c_void_p), ("x", _c_void_p), ("add", _c_void_p), ("y", _c_void_p),
-                ("N", _i64), ("K", _i64), ("epilogue", _int), ("source", _int), ("add_source", _int),
-                ("after", _int)]
-
-
-class Chain(ctypes.Structure):
-    """ftk_chain: a prepared chain (filled by ftk_chain_prepare)."""
-
-    _fields_ = [("workspace", _c_void_p), ("stages", _int), ("grid", _int), ("eps", _float),
-                ("stamps_offset", _i64)]
-
-
 class AttnConfig(ctypes.Structure):
     """ftk_attn_config: a decode-attention launch choice (kind, splits, waves, unroll); zeros = planner default."""
 
@@ -134,14 +119,6 @@ SIGNATURES = {
                                       _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
-    "ftk_chain_workspace_bytes": (_i64, [ctypes.POINTER(ChainStage), _int]),
-    "ftk_chain_prepare": (_int, [ctypes.POINTER(ChainStage), _int, _float, _c_void_p, _i64, ctypes.POINTER(Chain)]),
-    "ftk_chain_launch": (_int, [ctypes.POINTER(Chain), _c_void_p]),
-    "ftk_chain_status": (_int, [ctypes.POINTER(Chain)]),
-    "ftk_chain_stamps": (_int, [ctypes.POINTER(Chain), ctypes.POINTER(_i64)]),
-    "ftk_chain_plan": (_int, [ctypes.POINTER(ChainStage), _int, _int, ctypes.POINTER(_int), ctypes.POINTER(_int)]),
-    "ftk_chain_shape": (_int, [_int, ctypes.POINTER(_int), ctypes.POINTER(_int), ctypes.POINTER(_int),
-                               ctypes.POINTER(_int)]),
     "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
                                  ctypes.POINTER(_i64)]),
 }

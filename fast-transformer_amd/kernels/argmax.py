@@ -78,13 +78,20 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
             st = fused_project(inp, w, _native.EPI_ARGMAX, lg, norm_weight, eps, ids=tok, config=_as_config(choice))
             return lg if st == _native.FTK_OK else None
 
-        def native(w):
-            return argmax(F.linear(flat if norm_weight is None else rms_norm(flat, norm_weight, eps), w))
+        def native_logits(w, inp=flat):
+            return F.linear(inp if norm_weight is None else rms_norm(inp, norm_weight, eps), w)
 
-        choice = _choice("argmax", flat, weight, run, native, _native.EPI_ARGMAX, norm_weight is not None)
-        status = _native.FTK_ERR_UNSUPPORTED if choice == "native" else \
-            fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, ids=ids, top=top,
-                          config=_as_config(choice))
+        def native(w, inp=flat):
+            return argmax(native_logits(w, inp))
+
+        choice = _choice("argmax", flat, weight, run, native, _native.EPI_ARGMAX, norm_weight is not None,
+                         compare=native_logits)
+        if choice == "native":
+            # the form selection timed: torch's GEMM itself, never a second selection by linear()
+            full = native_logits(weight)
+            return argmax(full, top=top).to(ids_dtype), (full.reshape(*shape[:-1], v) if logits else None)
+        status = fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, ids=ids, top=top,
+                               config=_as_config(choice))
     else:
         status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
             fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,

@@ -13,7 +13,8 @@ one rounding to BF16 (linear.py:1-6). Under them:
   * M = 17..32: torch's native GEMM by default (hipBLASLt measured faster there),
     the way the reference keeps cuBLAS unless a timed kind beats it; the fused
     forms run their norm / epilogue kernels around it. An explicit config, or
-    FTK_TUNE=1 timing, still launches these kernels at any M.
+    the first-use timing of the candidates (on unless FTK_TUNE=0), still
+    launches these kernels at any M.
 
 ``split_ok`` is accepted for signature compatibility. The result is always a
 contiguous BF16 tensor, which the reference allows ("may be" a Split,
@@ -42,10 +43,10 @@ MAX_ROWS = _native.MAX_ROWS
 #: "native" = torch's GEMM (keep_native), or a launch tuple. _VALIDATED: the timed candidates.
 _CHOICES = {}
 _VALIDATED = {}
-#: Time the candidate launch shapes of each shape at first use (eager only), as linear.py:436-481
-#: does. Off by default (FTK_TUNE=1 or ``TUNE = True`` turns it on): the planner's defaults come
-#: from the same kind of timing, done once on MI355X.
-TUNE = os.environ.get("FTK_TUNE", "0") == "1"
+#: Time the candidate launch shapes of each shape at its first eager use, as linear.py:494-511
+#: always does. On by default; FTK_TUNE=0 (or ``TUNE = False``) keeps the planner's defaults, which
+#: come from the same kind of timing, done once on MI355X.
+TUNE = os.environ.get("FTK_TUNE", "1") != "0"
 
 #: From this many rows the planner's default is torch's native GEMM (hipBLASLt), as the reference
 #: keeps cuBLAS unless a timed kind beats it (linear.py:455-475). Measured on MI355X at Qwen3-8B
@@ -154,9 +155,15 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
         return y if status == _native.FTK_OK else None
 
     if config is None and _fusable(flat, weight, norm_weight):
-        choice = _choice("norm", flat, weight, lambda c, w, inp=flat: fused(_as_config(c), w, inp),
-                         lambda w: F.linear(rms_norm(flat, norm_weight, eps), w), prologue=True)
-        out = None if choice == "native" else fused(_as_config(choice), weight)
+        def native(w, inp=flat):
+            return F.linear(rms_norm(inp, norm_weight, eps), w)
+
+        choice = _choice("norm", flat, weight, lambda c, w, inp=flat: fused(_as_config(c), w, inp), native,
+                         prologue=True)
+        if choice == "native":
+            # the form selection timed: torch's GEMM itself, never a second selection by linear()
+            return native(weight).reshape(*shape[:-1], n)
+        out = fused(_as_config(choice), weight)
     else:
         out = None if prefer_native(m, config) else fused(config, weight)
     if out is None:
@@ -319,17 +326,19 @@ def _cold_us(fn, weights, reps=5):
 
 
 def _agrees(got, reference):
-    """Operator sanity check against the planner default: |Δ| <= 0.016 |ref| + 0.001 (linear.py:399-409)."""
+    """Operator sanity check against the native GEMM's output: |Δ| <= 0.016 |ref| + 0.001 (linear.py:399-409)."""
     got, ref = got.float(), reference.float()
     return bool(((got - ref).abs() <= ref.abs() * 0.016 + 0.001).all())
 
 
-def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=False):
+def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=False, compare=None):
     """Time the candidates of one shape once, eagerly (linear.py:436-481); returns the choice.
 
-    ``run(choice, w)`` computes the operation with a launch choice (None = planner default) on
-    weight ``w``; ``native(w)`` is the native-GEMM form. Every candidate must agree with the
-    planner default on a fixed probe input before it is timed.
+    ``run(choice, w, inp)`` computes the operation with a launch choice (None = planner default)
+    on weight ``w`` and input ``inp``; ``native(w, inp)`` is the native-GEMM form, and
+    ``compare(w, inp)`` (default ``native``) its output in the form ``run`` returns (the logits,
+    for lm_head + argmax). Every candidate, the planner default included, must agree with the
+    native output on a fixed probe input before it is timed (linear.py:452-453).
     """
     global _TUNING_DEADLINE, tuning_seconds
     m, k = x.shape
@@ -339,15 +348,14 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     if _TUNING_DEADLINE is None:
         _TUNING_DEADLINE = started + PROCESS_SECONDS
     if started >= _TUNING_DEADLINE:
-        return _inherit(op, x, weight, run)
+        return _inherit(op, x, weight, run, native, compare)
     copies = max(2, min(16, -(-COLD_BYTES // max(1, weight.numel() * weight.element_size()))))
     weights = [weight] + [weight.clone() for _ in range(copies - 1)]
     generator = torch.Generator(device=x.device).manual_seed(1729)
     probe = torch.randn(x.shape, device=x.device, dtype=x.dtype, generator=generator)
-    reference = run(None, weight, probe)
-    if reference is None:
+    if run(None, weight, probe) is None:
         return "native"
-    reference = reference.clone()
+    reference = (compare or native)(weight, probe).clone()
     deadline = min(_TUNING_DEADLINE, time.monotonic() + SHAPE_SECONDS)
     native_us = _cold_us(native, weights)
     best_us, best = native_us, "native"
@@ -355,10 +363,9 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     for choice in [None] + _candidates(m, n, k, epilogue, prologue):
         if time.monotonic() >= deadline:
             break
-        if choice is not None:
-            got = run(choice, weight, probe)
-            if got is None or not _agrees(got, reference):
-                continue
+        got = run(choice, weight, probe)
+        if got is None or not _agrees(got, reference):
+            continue
         us = _cold_us(lambda w, c=choice: run(c, w), weights)
         validated.append((us, choice))
         if us < best_us * 0.985:
@@ -382,13 +389,13 @@ def _choose(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
     return best
 
 
-def _inherit(op, x, weight, run):
+def _inherit(op, x, weight, run, native, compare=None):
     """The choice of a shape past the process budget (linear.py:412-433).
 
     A verify block (5..MAX_ROWS rows) takes a launch choice already frozen for the same operation
-    and weight shape at another row count above 4, if it agrees with the planner default on a probe
-    input (the launch must also exist at this row count). Otherwise, and for other row counts, the
-    shape takes its untuned default. The captured step's ``refine`` still re-judges the choice.
+    and weight shape at another row count above 4, if it agrees with the native GEMM's output on a
+    probe input (the launch must also exist at this row count). Otherwise, and for other row
+    counts, the shape takes its untuned default. The captured step's ``refine`` still re-judges it.
     """
     m, k = x.shape
     n = weight.shape[0]
@@ -400,10 +407,9 @@ def _inherit(op, x, weight, run):
         return default
     generator = torch.Generator(device=x.device).manual_seed(1729)
     probe = torch.randn(x.shape, device=x.device, dtype=x.dtype, generator=generator)
-    reference = run(None, weight, probe)
-    if reference is None:
+    if run(None, weight, probe) is None:
         return default
-    reference = reference.clone()
+    reference = (compare or native)(weight, probe).clone()
     for other, choice in list(_CHOICES.items()):
         if choice in (None, "native") or _key(op, x.device, other[-3], n, k) != other:
             continue  # a default, or another operation, device or weight shape
@@ -421,8 +427,11 @@ def _inherit(op, x, weight, run):
     return default
 
 
-def _choice(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=False):
-    """The frozen launch choice of a call with no explicit config, selected on first use when tuning is on."""
+def _choice(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=False, compare=None):
+    """The frozen launch choice of a call with no explicit config, selected on first use when tuning is on.
+
+    A first use during graph capture raises RuntimeError, as linear.py:497-498 does. A "native"
+    choice means the caller runs ``native`` itself (torch's GEMM), the form that was timed."""
     m, k = x.shape
     n = weight.shape[0]
     key = _key(op, x.device, m, n, k)
@@ -430,7 +439,7 @@ def _choice(op, x, weight, run, native, epilogue=_native.EPI_STORE, prologue=Fal
         if TUNE:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("projection selection must finish during eager warmup")
-            _CHOICES[key] = _choose(op, x, weight, run, native, epilogue, prologue)
+            _CHOICES[key] = _choose(op, x, weight, run, native, epilogue, prologue, compare)
             # Re-judging order = weight traffic per step: the vocabulary projection runs once per
             # step, every other projection once per layer (linear.py:515-520). The planner default
             # always stays an option, so a captured step can fall back to it.
@@ -521,7 +530,7 @@ def linear(x, weight, split_ok=False):
     def run(choice, w, inp=flat):
         return project(inp, w, _as_config(choice))
 
-    choice = _choice("linear", flat, weight, run, lambda w: F.linear(flat, w))
+    choice = _choice("linear", flat, weight, run, lambda w, inp=flat: F.linear(inp, w))
     if choice == "native":
         return F.linear(x, weight)
     out = project(flat, weight, _as_config(choice))

@@ -68,12 +68,15 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
             st = fused_project(inp, w, _native.EPI_SWIGLU, y, norm_weight, eps, config=_as_config(choice))
             return y if st == _native.FTK_OK else None
 
-        def native(w):
-            return swiglu(F.linear(flat if norm_weight is None else rms_norm(flat, norm_weight, eps), w))
+        def native(w, inp=flat):
+            return swiglu(F.linear(inp if norm_weight is None else rms_norm(inp, norm_weight, eps), w))
 
         choice = _choice("swiglu", flat, gate_up_weight, run, native, _native.EPI_SWIGLU, norm_weight is not None)
-        status = _native.FTK_ERR_UNSUPPORTED if choice == "native" else \
-            fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, config=_as_config(choice))
+        if choice == "native":
+            # the form selection timed: torch's GEMM itself, never a second selection by linear()
+            return native(gate_up_weight).reshape(*shape[:-1], n // 2)
+        status = fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps,
+                               config=_as_config(choice))
     else:
         status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
             fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,

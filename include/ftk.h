@@ -22,12 +22,8 @@
  *   - Workspaces hold per-call scratch only (per-workgroup argmax keys,
  *     RMSNorm row scales): no initial contents are required and nothing carries
  *     over between calls. Calls that share a workspace must not run
- *     concurrently. No projection, norm, attention or argmax kernel waits on
- *     another workgroup: they use no device-scope fences or tickets. The one
- *     exception is the projection chain (ftk_chain_*): a cooperative launch
- *     whose workgroups wait, with bounded polls, for words other workgroups
- *     of the same launch store; its workspace carries an epoch between
- *     launches (set up by ftk_chain_prepare).
+ *     concurrently. No kernel waits on another workgroup: they use no
+ *     device-scope fences or tickets.
  */
 #ifndef FTK_H
 #define FTK_H
@@ -232,67 +228,6 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
  * of rmsnorm.py:98-125. cfg may be NULL. */
 int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
                          int64_t K, const ftk_config* cfg, void* stream);
-
-/* ---- projection chains (one launch for a list of dependent M = 1 projections) ---- */
-/* A decode step's projections in the reference are separate launches in one captured graph,
- * overlapped on H100 by programmatic dependent launch (engine/decode.py:650-668,
- * engine/kernels/pdl.py:1-42). A chain runs a list of them -- the QKV, O, gate/up + SwiGLU and
- * down projections of engine/layers.py:44, :86, :101-102 with the norms and residual adds of
- * engine/decode.py:229-261, for one layer or many -- as ONE cooperative launch (one workgroup
- * per CU): each workgroup issues its next weight window before it waits for that stage's input,
- * and outputs pass between workgroups as tagged words with bounded waits. Per stage the
- * arithmetic is that of ftk_project_rows_bf16 / ftk_project_add_bf16 at M = 1 (FP32 sums, one
- * BF16 rounding, the RMSNorm cast order of engine/kernels/rmsnorm.py:35-46, the SwiGLU of
- * engine/kernels/swiglu.py:20-24); sums may be ordered differently, so results agree with those
- * entry points within a BF16 ulp, not bit for bit. M = 1 only. */
-#define FTK_CHAIN_MAX_STAGES 1024
-
-typedef struct ftk_chain_stage {
-  const void* w;      /* [N, K] BF16 weight (W = cat(W_gate, W_up) for SwiGLU), 16-byte aligned */
-  const void* gamma;  /* [K] RMSNorm gain of the input (prologue), or NULL */
-  const void* x;      /* [K] external BF16 input, 16-byte aligned; NULL when `source` >= 0 */
-  const void* add;    /* [N_out] external BF16 residual added in the epilogue, or NULL */
-  void* y;            /* [N_out] BF16 output, or NULL (the chain keeps its own copy for later stages) */
-  int64_t N, K;       /* N_out = N, or N / 2 with SwiGLU; K % 512 == 0 in the built shapes, K <= 12288 */
-  int epilogue;       /* FTK_EPI_STORE or FTK_EPI_SWIGLU (no residual with SwiGLU) */
-  int source;         /* earlier stage whose output is this stage's input, or -1 (use x) */
-  int add_source;     /* earlier stage whose output is the residual: y = bf16(bf16(x W^T) + r), or -1 */
-  int after;          /* earlier stage that must have finished before this one starts, or -1 (work
-                         outside the chain between them, e.g. attention between QKV and O) */
-} ftk_chain_stage;
-
-typedef struct ftk_chain {  /* filled by ftk_chain_prepare */
-  void* workspace;
-  int stages;
-  int grid;                 /* workgroups: one per CU */
-  float eps;                /* RMSNorm epsilon of every prologue */
-  int64_t stamps_offset;    /* byte offset of the per-stage clock stamps in the workspace */
-} ftk_chain;
-
-/* Workspace bytes for this chain on the current device (-1: invalid or unsupported). */
-int64_t ftk_chain_workspace_bytes(const ftk_chain_stage* stages, int n_stages);
-/* Validate the stages, plan each one, and write the chain's device program into `workspace`
- * (256-byte aligned, ftk_chain_workspace_bytes of it); clears its control words. Synchronous:
- * call it outside graph capture. The stage pointers are baked in: a launch reads and writes the
- * same tensors every time. */
-int ftk_chain_prepare(const ftk_chain_stage* stages, int n_stages, float eps, void* workspace,
-                      int64_t workspace_bytes, ftk_chain* chain);
-/* Enqueue one run of the chain on `stream` (cooperative launch; capture-safe). */
-int ftk_chain_launch(const ftk_chain* chain, void* stream);
-/* Synchronizes the device, then returns 0 when every launch so far finished, or 1 + the index of
- * the stage whose bounded wait expired (that launch stopped, and later launches exit at once
- * until ftk_chain_prepare runs again); -1 on a HIP error. */
-int ftk_chain_status(const ftk_chain* chain);
-/* Synchronizes, then copies the real-time clock stamps (100 MHz) of the last launch,
- * out[(3 stages + 1) * grid]: for stage s and workgroup g, out[3 s grid + g] = when g began the
- * stage, out[(3 s + 1) grid + g] = when its input row was in place (0 if g had no tile),
- * out[(3 s + 2) grid + g] = when g finished it; out[3 stages grid + g] = when g started. */
-int ftk_chain_stamps(const ftk_chain* chain, int64_t* out);
-/* Host only: the shape and tile count each stage would get on `compute_units` CUs. */
-int ftk_chain_plan(const ftk_chain_stage* stages, int n_stages, int compute_units, int* shapes, int* tiles);
-/* Host only: what a shape id means (16-byte chunks per lane per row, waves per row group, weight
- * rows per group per tile, epilogue). */
-int ftk_chain_shape(int shape, int* c, int* kw, int* rows_per_group, int* epilogue);
 
 /* ---- standalone operators ---------------------------------------------------- */
 

@@ -1,5 +1,12 @@
-"""Shared test setup: the `gpu` marker, import paths, BF16 bit helpers."""
+"""Shared test setup: the `gpu` marker, import paths, BF16 bit helpers.
 
+The library times each new shape's launch candidates on first use by default (kernels/linear.py
+TUNE, as engine/kernels/linear.py:494-511 does). Parity tests check particular kernels, so this
+session keeps the planner's defaults unless FTK_TUNE is set; tests/test_gpu_select.py turns the
+selection on itself and runs the default policy in a fresh process.
+"""
+
+import os
 import sys
 from pathlib import Path
 
@@ -14,6 +21,8 @@ for path in (str(ROOT), str(PKG)):
         sys.path.insert(0, path)
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
+
+os.environ.setdefault("FTK_TUNE", "0")
 
 
 def pytest_configure(config):

@@ -8,7 +8,16 @@ knobs), the reference's policy of engine/kernels/linear.py:317-486 and engine/de
 - A first use during graph capture raises RuntimeError (linear.py:497-498).
 - ``refine`` re-judges the knobs inside a captured step; the graph captured with its final choices
   replays bit for bit as the eager step.
+- Selection is on by default: a fresh process without FTK_TUNE selects on first use and raises on a
+  first use under capture. A fused operation whose knob is put on "native" runs torch's GEMM
+  directly, so capturing it needs no further selection.
 """
+
+import os
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -164,3 +173,87 @@ def test_past_the_process_budget_a_verify_block_inherits(cuda, tuning, monkeypat
     y3 = L.linear(x3, w)
     assert L._CHOICES[(cuda, 3, 4096, 4096)] is None and L.inherited[(cuda, 3, 4096, 4096)] is None
     assert within(to_bits(y3), path.project(to_bits(x3), to_bits(w)))
+
+
+DEFAULT_POLICY = textwrap.dedent("""
+    import sys, torch
+    sys.path.insert(0, sys.argv[1])
+    from kernels import linear as L, tune
+    assert L.TUNE, "selection must be on by default"
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((1, 1024), generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn((512, 1024), generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    y = L.linear(x, w)
+    key = (dev, 1, 512, 1024)
+    assert key in L._CHOICES and L._VALIDATED[key], "first use did not select"
+    assert any(k.name == key for k in tune.knobs(1)), "no knob registered"
+    ref = torch.nn.functional.linear(x, w).float()
+    assert bool(((y.float() - ref).abs() <= ref.abs() * 0.016 + 0.001).all())
+    x2 = torch.randn((1, 1024), generator=g).to(torch.bfloat16).to(dev)
+    w2 = (torch.randn((256, 1024), generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                L.linear(x2, w2)
+    except RuntimeError as e:
+        assert "eager warmup" in str(e), e
+        print("default policy ok", flush=True)
+    else:
+        raise AssertionError("a first use under capture did not raise")
+    torch.cuda.synchronize()
+""")
+
+
+def test_selection_is_on_by_default_in_a_fresh_process(cuda):
+    env = {k: v for k, v in os.environ.items() if k != "FTK_TUNE"}
+    env["FTK_TUNE_SECONDS"] = "10"
+    pkg = str(Path(__file__).resolve().parents[1] / "fast-transformer_amd")
+    print("test_selection_is_on_by_default_in_a_fresh_process: child process starts", flush=True)
+    proc = subprocess.run([sys.executable, "-c", DEFAULT_POLICY, pkg], env=env, capture_output=True, text=True,
+                          timeout=100)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert "default policy ok" in proc.stdout
+
+
+@pytest.mark.parametrize("op", ["norm", "swiglu", "argmax"])
+def test_a_fused_knob_on_native_captures_without_eager_warmup(cuda, tuning, op):
+    """A fused operation whose frozen choice is "native" runs torch's GEMM itself (the form its
+    selection timed): capturing it needs no selection of a plain projection key."""
+    h = 1024
+    x = seeded((1, h), 51, device=cuda)
+    g = seeded((h,), 52, scale=0.1, shift=1.0, device=cuda)
+    n = {"norm": 2048, "swiglu": 2 * 3072, "argmax": 8192}[op]
+    w = seeded((n, h), 53, scale=0.02, device=cuda)
+    from kernels import argmax as A
+    from kernels.rmsnorm import rms_norm
+
+    def call():
+        if op == "norm":
+            return L.rms_norm_linear(x, g, EPS, w)
+        if op == "swiglu":
+            return S.gate_up_swiglu(x, w, g, EPS)
+        return A.lm_head_argmax(x, w, g, EPS, logits=True)[1]
+
+    call()  # eager first use: selects under the fused key
+    key = (op, cuda, 1, n, h)
+    assert key in L._CHOICES
+    L._CHOICES[key] = "native"  # what refine does when it keeps the native option
+    plain = [k for k in L._CHOICES if not isinstance(k[0], str)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            out = call()
+    torch.cuda.synchronize()
+    assert [k for k in L._CHOICES if not isinstance(k[0], str)] == plain, "a plain projection was selected"
+    logits = torch.nn.functional.linear(rms_norm(x, g, EPS), w)
+    want = {"norm": logits, "swiglu": S.swiglu(logits), "argmax": logits}[op]
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_bits(out), to_bits(want))

@@ -33,6 +33,11 @@ def _run(bad=(), missing=()):
     return run
 
 
+def _native_gemm(w, inp):
+    """The native GEMM's output, the reference every inherited choice must agree with."""
+    return inp.float() @ w.float().T
+
+
 def _operands(m, n=64, k=32):
     g = torch.Generator().manual_seed(m)
     return torch.randn((m, k), generator=g).to(torch.bfloat16), torch.randn((n, k), generator=g).to(torch.bfloat16)
@@ -41,7 +46,7 @@ def _operands(m, n=64, k=32):
 def test_past_the_budget_a_verify_block_inherits_an_agreeing_choice(fresh):
     x, w = _operands(5)
     L._CHOICES[(DEV, 8, 64, 32)] = RING
-    assert L._choose("linear", x, w, _run(), None) == RING
+    assert L._choose("linear", x, w, _run(), _native_gemm) == RING
     assert L.inherited[(DEV, 5, 64, 32)] == RING
     assert L._VALIDATED[(DEV, 5, 64, 32)][0] == (0.0, RING)
 
@@ -50,7 +55,7 @@ def test_a_choice_that_disagrees_or_does_not_exist_is_not_inherited(fresh):
     x, w = _operands(5)
     L._CHOICES[(DEV, 8, 64, 32)] = RING
     L._CHOICES[(DEV, 16, 64, 32)] = QUAD
-    assert L._choose("linear", x, w, _run(bad=(RING,), missing=(QUAD,)), None) is None
+    assert L._choose("linear", x, w, _run(bad=(RING,), missing=(QUAD,)), _native_gemm) is None
     assert L.inherited[(DEV, 5, 64, 32)] is None
 
 
@@ -60,9 +65,9 @@ def test_only_the_same_operation_and_weight_shape_at_more_than_4_rows(fresh):
     L._CHOICES[(DEV, 8, 128, 32)] = RING             # another weight shape
     L._CHOICES[("norm", DEV, 8, 64, 32)] = RING      # another operation
     L._CHOICES[(DEV, 12, 64, 32)] = "native"          # native is not a launch choice
-    assert L._choose("linear", x, w, _run(), None) is None
+    assert L._choose("linear", x, w, _run(), _native_gemm) is None
     L._CHOICES[("norm", DEV, 8, 64, 32)] = QUAD
-    assert L._choose("norm", x, w, _run(), None) == QUAD
+    assert L._choose("norm", x, w, _run(), _native_gemm) == QUAD
 
 
 @pytest.mark.parametrize("m,default,missing", [(3, None, ()), (1, None, ()), (40, "native", ()),
@@ -72,5 +77,5 @@ def test_other_row_counts_take_their_untuned_default(fresh, m, default, missing)
     that exists there (RING stops at 16 rows), else take the native GEMM."""
     x, w = _operands(m)
     L._CHOICES[(DEV, 8, 64, 32)] = RING
-    assert L._choose("linear", x, w, _run(missing=missing), None) == default
+    assert L._choose("linear", x, w, _run(missing=missing), _native_gemm) == default
     assert L._VALIDATED[(DEV, m, 64, 32)] == [(0.0, default)]
