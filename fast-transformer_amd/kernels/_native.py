@@ -215,7 +215,8 @@ def argmax_workspace(device, rows, vocab):
     return workspace(device, int(lib().ftk_argmax_workspace_bytes(rows, vocab)), "argmax")
 
 
-def project_workspace(device, m, n, k, epilogue, config=None, prologue=False):
-    """Workspace of one projection call (row scales, argmax keys); ``prologue``: the call has gamma."""
-    flags = epilogue | (PLAN_PROLOGUE if prologue else 0)
+def project_workspace(device, m, n, k, epilogue, config=None, prologue=False, residual=False):
+    """Workspace of one projection call (row scales, argmax keys); ``prologue``: the call has gamma;
+    ``residual``: its prologue adds a residual, which the planner plans on other kinds and grids."""
+    flags = epilogue | (PLAN_PROLOGUE if prologue else 0) | (PLAN_RESIDUAL if residual else 0)
     return workspace(device, int(lib().ftk_project_workspace_bytes(m, n, k, flags, config)), "project")

@@ -92,7 +92,8 @@ def fused_project(x, weight, epilogue, out, norm_weight=None, eps=1e-6, residual
         table_rows = x.shape[0] if x_ids is not None else 0
         rows = ctypes.byref(_native.Rows(_native.ptr(residual), _native.ptr(summed), _native.ptr(x_ids), ids_bytes,
                                          table_rows))
-    ws = _native.project_workspace(x.device, m, n, k, epilogue, config, prologue=norm_weight is not None)
+    ws = _native.project_workspace(x.device, m, n, k, epilogue, config, prologue=norm_weight is not None,
+                                   residual=residual is not None)
     ids_bytes = 0 if ids is None else {torch.int64: 8, torch.int32: 4}[ids.dtype]
     status = _native.try_call(
         "ftk_project_rows_bf16", _native.ptr(x), rows, _native.ptr(norm_weight), float(eps), _native.ptr(weight),

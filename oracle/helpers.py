@@ -4,6 +4,9 @@
 compute units; the C library's planner runs the same rule
 (``ftk_persistent_programs``, csrc/ftk_plan.h) and tests/test_oracle.py checks
 the library's function against this one and the reference's known answers.
+``exact_splits`` is the reference's split-K count rule; nothing in this build
+splits K across workgroups, so it has no counterpart in the library and is kept
+here, pinned to the reference's known answers, for the record of the rule.
 """
 
 
@@ -31,3 +34,18 @@ def tile_owners(tiles, programs):
         for t in range(p, tiles, programs):
             owners[t] += 1
     return owners
+
+
+def exact_splits(k, block_k, wanted):
+    """Split count for K in whole BLOCK_K blocks: the largest count <= ``wanted`` that divides the
+    block count, so that no split program is left without a block (engine/kernels/gemm.py:428-433;
+    known answers at engine/kernels/linear.py:359-361 with 128-wide blocks and 8 wanted: K = 2560 ->
+    5, K = 9728 -> 4). A K that is not a whole number of blocks keeps ``wanted``.
+    """
+    if k % block_k:
+        return wanted
+    blocks = k // block_k
+    splits = wanted
+    while blocks % splits:
+        splits -= 1
+    return splits

@@ -439,3 +439,19 @@ def test_native_gemm_from_seventeen_rows_without_a_config():
     assert L.NATIVE_FROM_ROWS == 17
     assert not L.prefer_native(16) and L.prefer_native(17) and L.prefer_native(32)
     assert not L.prefer_native(32, _native.Config(_native.KIND_MFMA, 0, 0, 0, 0))
+
+
+@pytest.mark.parametrize("m", [5, 8, 16])
+def test_residual_calls_size_the_workspace_of_their_own_plan(m):
+    """A call whose prologue adds a residual is planned on another kind and grid than the same call
+    without it (RING does not take the add); the workspace is sized from that plan, so its argmax
+    keys (one per workgroup and row) always fit."""
+    flags = _native.EPI_ARGMAX | _native.PLAN_PROLOGUE
+    plain = _native.lib().ftk_project_workspace_bytes(m, 151936, 4096, flags, None)
+    with_residual = _native.lib().ftk_project_workspace_bytes(m, 151936, 4096, flags | _native.PLAN_RESIDUAL, None)
+    p = _native.Plan()
+    _native.call("ftk_plan_project", m, 151936, 4096, flags | _native.PLAN_RESIDUAL, 256, None, p)
+    assert p.kind != _native.KIND_RING
+    assert with_residual == p.workspace_bytes >= 256 + 8 * m * p.grid
+    _native.call("ftk_plan_project", m, 151936, 4096, flags, 256, None, p)
+    assert p.kind == _native.KIND_RING and plain == p.workspace_bytes

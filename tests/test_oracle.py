@@ -245,6 +245,29 @@ def test_persistent_programs_known_answers():
         assert helpers.persistent_programs(tiles, 132) == tiles
 
 
+def test_exact_splits_known_answers():
+    # engine/kernels/linear.py:359-361: 128-wide K blocks, the power-of-two split count 8
+    assert helpers.exact_splits(2560, 128, 8) == 5
+    assert helpers.exact_splits(9728, 128, 8) == 4
+    assert helpers.exact_splits(4096, 128, 8) == 8
+    assert helpers.exact_splits(4100, 128, 8) == 8  # not whole blocks: the wanted count stays
+
+
+def test_exact_splits_against_a_simulated_split_layout():
+    """Brute force: lay the K blocks out over s split programs of ceil(blocks / s) contiguous blocks
+    each; the rule's answer is the largest s <= wanted whose programs all get the same, non-zero
+    number of blocks (no partial and no dead split program)."""
+    for blocks in range(1, 97):
+        for wanted in range(1, 17):
+            exact = []
+            for s in range(1, wanted + 1):
+                chunk = -(-blocks // s)
+                counts = [max(0, min((i + 1) * chunk, blocks) - i * chunk) for i in range(s)]
+                if all(c == chunk for c in counts):
+                    exact.append(s)
+            assert helpers.exact_splits(blocks * 64, 64, wanted) == max(exact), (blocks, wanted)
+
+
 def test_tile_owners_each_once():
     for tiles, units in ((304, 132), (2374, 132), (9496, 256), (17, 256)):
         programs = helpers.persistent_programs(tiles, units)
