@@ -434,6 +434,10 @@ def main():
     ap.add_argument("--profile-attention", type=int, default=0, metavar="PASSES",
                     help="profiling mode: PASSES eager passes of decode attention, then of rope_attend, over each "
                          "ATTN_CASES cache set (distinct caches), then one 1 GiB device copy as the counter reference")
+    ap.add_argument("--profile-kernels", type=int, default=0, metavar="PASSES",
+                    help="profiling mode: PASSES eager passes of each bandwidth-bound configuration's kernels "
+                         "(C3 layers, C5 at M=1 and 5, C2 layers, C1) on the planner's defaults, then one 1 GiB "
+                         "device copy as the counter reference")
     ap.add_argument("--profile-rows", type=str, default="", metavar="M[,M...]",
                     help="profiling mode: two eager passes of the 36-layer projection set at each M rows "
                          "(the C4 workload), then one 1 GiB device copy as the counter reference")
@@ -450,6 +454,9 @@ def main():
     _native.lib()
 
     cfg = QWEN3_8B
+    if args.profile_kernels:
+        profile_kernels(dev, args.profile_kernels)
+        return
     if args.profile_gate_up:
         profile_gate_up(cfg, dev, args.profile_gate_up)
         return
@@ -529,7 +536,9 @@ def main():
 
 
 def profile_gate_up(cfg, dev, passes):
-    """Eager launches of the dominant kernel only (for rocprofv3 counter runs), plus a copy of known size."""
+    """Eager launches of the dominant kernel only, on the planner's default (for rocprofv3 counter runs),
+    plus a copy of known size."""
+    L.TUNE = False
     g = torch.Generator(device=dev).manual_seed(0)
     h, i = cfg["hidden"], cfg["inter"]
     weights = [(torch.randn((2 * i, h), generator=g, device=dev) * 0.02).to(torch.bfloat16)
@@ -551,7 +560,9 @@ def profile_gate_up(cfg, dev, passes):
 
 def profile_rows(cfg, dev, rows):
     """Eager passes of the 36-layer projection set at M rows (for rocprofv3 counter runs), plus a
-    copy of known size. Each layer is RMSNorm-prologue QKV, O, RMSNorm-prologue gate/up + SwiGLU, down."""
+    copy of known size. Each layer is RMSNorm-prologue QKV, O, RMSNorm-prologue gate/up + SwiGLU, down,
+    on the planner's defaults."""
+    L.TUNE = False
     model = Model(cfg, dev, head=False)
     for m in rows:
         step = Step(model, m, dev, seed=m)
@@ -570,6 +581,56 @@ def profile_rows(cfg, dev, rows):
 
 #: Distinct lm_head weight copies timed in one graph for C5 (1.24 GB each).
 C5_COPIES = 4
+
+#: Dispatch order of --profile-kernels: (label, projections per layer or call, layers or copies).
+PROFILE_KERNELS = (("C3 8B M=1", ("qkv", "o", "gate_up", "down"), 36),
+                   ("C5 M=1", ("lm_head",), C5_COPIES),
+                   ("C5 M=5", ("lm_head",), C5_COPIES),
+                   ("C2 0.6B M=1", ("qkv", "o", "gate_up", "down"), 28),
+                   ("C1 0.6B qkv M=1 (no prologue)", ("qkv",), 64))
+
+
+def profile_kernels(dev, passes=2):
+    """Eager passes of every bandwidth-bound BASELINE configuration's kernels on the planner's
+    defaults (for rocprofv3 counter runs), in the order of PROFILE_KERNELS, then a 1 GiB copy as the
+    counter reference. All weights are made first, so the projection launches are the only ftk
+    dispatches, ``passes`` times each: C3's 36 layers (QKV, O, gate/up + SwiGLU, down), C5's lm_head
+    + argmax at M = 1 and 5 over C5_COPIES weight copies (projection, then the argmax finalize),
+    C2's 28 layers, C1's QKV projection without the norm over 64 weight copies."""
+    L.TUNE = False
+    model8 = Model(QWEN3_8B, dev, head=True)
+    step8 = Step(model8, 1, dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    heads = [model8.head] + [(torch.randn((QWEN3_8B["vocab"], QWEN3_8B["hidden"]), generator=gen, device=dev) * 0.02)
+                             .to(torch.bfloat16) for _ in range(C5_COPIES - 1)]
+    h_rows = {m: torch.randn((m, QWEN3_8B["hidden"]), generator=gen, device=dev).to(torch.bfloat16) for m in (1, 5)}
+    top = torch.empty(5, dtype=torch.float32, device=dev)
+    model06 = Model(QWEN3_06B, dev, head=False, seed=2)
+    step06 = Step(model06, 1, dev, seed=3)
+    x = torch.randn((1, 1024), generator=gen, device=dev).to(torch.bfloat16)
+    copies = [(torch.randn((4096, 1024), generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(64)]
+    ys = [torch.empty((1, 4096), device=dev, dtype=torch.bfloat16) for _ in range(64)]
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    runs = {"C3 8B M=1": step8.layers,
+            "C5 M=1": lambda: [A.lm_head_argmax(h_rows[1], w, model8.final_norm, EPS, logits=True, top=top[:1],
+                                                ids_dtype=torch.int32) for w in heads],
+            "C5 M=5": lambda: [A.lm_head_argmax(h_rows[5], w, model8.final_norm, EPS, logits=True, top=top,
+                                                ids_dtype=torch.int32) for w in heads],
+            "C2 0.6B M=1": step06.layers,
+            "C1 0.6B qkv M=1 (no prologue)": lambda: [L.project(x, w, out=y) for w, y in zip(copies, ys)]}
+    for label, _, _ in PROFILE_KERNELS:
+        for _ in range(passes):
+            runs[label]()
+        torch.cuda.synchronize()
+        stage(f"profile {label}: {passes} passes")
+    dst.copy_(src)  # reference kernel: reads and writes exactly 1 GiB
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "profile-kernels", "passes": passes, "order": PROFILE_KERNELS, "copy_bytes": 1 << 30,
+                      "bytes": {"C3": layer_bytes(QWEN3_8B, 1), "C2": layer_bytes(QWEN3_06B, 1),
+                                "C5 M=1": head_bytes(QWEN3_8B, 1), "C5 M=5": head_bytes(QWEN3_8B, 5),
+                                "C1": 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096}}), flush=True)
 
 
 def shapes_table(model8, step8, dev):
