@@ -183,9 +183,12 @@ def tuned_graph(fn, rows, seconds, label):
     return capture(fn)
 
 
-def time_graph(graph, reps=10, inner=1, warm_s=0.0):
+def time_graph(graph, reps=10, inner=1, warm_s=None):
     """Median wall time of one replay, from HIP events on the replay stream (µs). ``warm_s``: replay
-    untimed for that long first, so that the GPU's clocks have settled as they have mid-run."""
+    untimed for that long first (default LAYER_WARM_S), so that every timing sees the clocks of a GPU
+    that is already busy, wherever it falls in the run."""
+    if warm_s is None:
+        warm_s = LAYER_WARM_S
     graph.replay()
     torch.cuda.synchronize()
     t_end = time.monotonic() + warm_s
@@ -237,6 +240,41 @@ def shape_entry(us, byts, flops=None):
     return e
 
 
+#: Launch shapes of the pure streaming read (ftk_stream_read) tried for each floor: persistent
+#: workgroups per CU (0: one-shot workgroups, the form of the projections that walk one tile per
+#: workgroup) and 16-byte loads in flight per lane.
+FLOOR_SHAPES = tuple((gpc, loads) for gpc in (1, 2, 4, 8) for loads in (2, 4, 8)) + \
+    tuple((0, loads) for loads in (2, 4, 8, 16))
+
+
+def read_floor(tensors, reps=5):
+    """The fastest pure streaming read of ``tensors`` (ftk_stream_read: the projections' load path and
+    nothing else), one launch per tensor in one graph, the same bytes and the same graph form as the
+    projections that read them: (µs per launch, (workgroups per CU, loads per lane) that gave it)."""
+    dev = tensors[0].device
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    most = max(t.numel() * t.element_size() for t in tensors)
+    sink = torch.empty(max(8 * cus, -(-most // (4096 * 2))), dtype=torch.int32, device=dev)
+    best = None
+    for gpc, loads in FLOOR_SHAPES:
+        def fn():
+            for t in tensors:
+                _native.call("ftk_stream_read", _native.ptr(t), t.numel() * t.element_size(), _native.ptr(sink),
+                             gpc * cus, loads, _native.stream_of(t))
+        us = time_graph(capture(fn, warm=1), reps=reps, warm_s=0.1) / len(tensors)
+        if best is None or us < best[0]:
+            best = (us, (gpc, loads))
+    return best
+
+
+def floor_entry(entry, floor):
+    """A per_shape entry with the read floor of its bytes beside it."""
+    us, (gpc, loads) = floor
+    shape = f"{gpc} workgroups per CU" if gpc else "one-shot workgroups"
+    return {**entry, "read_floor_us": round(us, 3), "over_floor_us": round(entry["us"] - us, 3),
+            "floor_shape": f"{shape}, {loads} loads per lane"}
+
+
 def planner_config(m, n, k, epilogue, prologue):
     """The planner's default launch for a shape as an explicit config (no selection involved)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -248,7 +286,7 @@ def planner_config(m, n, k, epilogue, prologue):
     return cfg
 
 
-def per_kind(step, kind, warm=2, config=None, warm_s=0.0):
+def per_kind(step, kind, warm=2, config=None, warm_s=None):
     """One graph of the 36 (or 28) launches of one projection kind, distinct weights each; µs per launch.
     ``config`` pins the gate/up launch (otherwise each call takes its frozen choice)."""
     def fn():
@@ -274,6 +312,9 @@ def per_kind(step, kind, warm=2, config=None, warm_s=0.0):
 
 #: Untimed replays before the roofline kernel's timed ones (seconds).
 ROOFLINE_WARM_S = 0.5
+#: Untimed replays before each graph is timed (seconds): every timing then sees the clocks of a GPU
+#: that is already busy, wherever it falls in the run.
+LAYER_WARM_S = 0.3
 
 
 def roofline(step):
@@ -505,7 +546,7 @@ def main():
     per_shape = {}
     stage(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
     if not args.no_shapes:
-        per_shape = shapes_table(model, step, dev)
+        per_shape = shapes_table(model, step, dev, layer_graph)
         per_shape.update(attention_table(cfg, dev))
         if args.extras:
             per_shape.update(full_layer_table(model, dev))
@@ -528,11 +569,17 @@ def main():
         "selection": selection_summary(),
     }
     if per_shape:
+        result["layer_read_floor_us"] = per_shape["C3 8B layer M=1"]["read_floor_us"]
         result["per_shape"] = per_shape
     if not args.no_cpu:
         stage("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(model, dev, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    # Leave nothing to the exit handlers: the captured graphs and the cached blocks are released
+    # here, while the HIP runtime (and a profiler's hooks into it) is still fully up.
+    del graph, layer_graph
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
 
 def profile_gate_up(cfg, dev, passes):
@@ -633,15 +680,18 @@ def profile_kernels(dev, passes=2):
                                 "C1": 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096}}), flush=True)
 
 
-def shapes_table(model8, step8, dev):
-    """µs / GB/s / fraction of the HBM roofline for every BASELINE.json configuration (C1-C5)."""
+def shapes_table(model8, step8, dev, layer_graph):
+    """µs / GB/s / fraction of the HBM roofline for every BASELINE.json configuration (C1-C5), each
+    M = 1 projection with the pure-read floor of its bytes (``read_floor``) beside it."""
     out = {}
     cfg = model8.cfg
     lb = layer_bytes(cfg, 1)
+    floors = {}
     for kind in ("qkv", "o", "gate_up", "down"):
         us = per_kind(step8, kind)
-        out[f"C3 8B {kind} M=1"] = shape_entry(us, lb[kind])
-    stage("C3 per-projection timings done")
+        floors[kind] = read_floor([lw[kind] for lw in model8.layers])
+        out[f"C3 8B {kind} M=1"] = floor_entry(shape_entry(us, lb[kind]), floors[kind])
+    stage("C3 per-projection timings and read floors done")
     # C5: lm_head + argmax at M=1 and M=5, over C5_COPIES distinct weight copies per graph (5 GB:
     # nothing is served from the MALL, and a graph launch is not charged to a single call)
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -655,6 +705,9 @@ def shapes_table(model8, step8, dev):
         us = time_graph(g) / len(heads)
         out[f"C5 lm_head+argmax M={m}"] = shape_entry(us, head_bytes(cfg, m), 2 * m * cfg["vocab"] * cfg["hidden"])
         stage(f"C5 M={m} done")
+    head_floor = read_floor(heads, reps=3)
+    for m in (1, 5):
+        out[f"C5 lm_head+argmax M={m}"] = floor_entry(out[f"C5 lm_head+argmax M={m}"], head_floor)
     del heads
     # C4: 8B layer set at M = 5, 8, 16
     for m in (5, 8, 16):
@@ -667,10 +720,11 @@ def shapes_table(model8, step8, dev):
         stage(f"C4 M={m} done")
     out.update(vendor_table(model8, dev))
     stage("C4 projections against hipBLASLt done")
-    # C3 per layer (M=1)
-    g = capture(step8.layers)
-    us = time_graph(g, reps=5) / cfg["layers"]
-    out["C3 8B layer M=1"] = shape_entry(us, sum(lb.values()))
+    # C3 per layer (M=1): the headline's own layer graph, timed again late in the run
+    us = time_graph(layer_graph, reps=10) / cfg["layers"]
+    floor_us = sum(f[0] for f in floors.values())
+    out["C3 8B layer M=1"] = {**shape_entry(us, sum(lb.values())), "read_floor_us": round(floor_us, 3),
+                              "over_floor_us": round(us - floor_us, 3)}
     # ... and in the decode data flow: both norms also add the residual and store the new stream
     g = capture(step8.layers_residual)
     us = time_graph(g, reps=5) / cfg["layers"]
@@ -685,13 +739,16 @@ def shapes_table(model8, step8, dev):
     st06 = Step(model06, 1, dev, seed=3)
     g = capture(st06.layers)
     us = time_graph(g, reps=10) / QWEN3_06B["layers"]
-    out["C2 0.6B layer M=1"] = shape_entry(us, sum(layer_bytes(QWEN3_06B, 1).values()))
+    floor_us = sum(read_floor([lw[kind] for lw in model06.layers])[0] for kind in ("qkv", "o", "gate_up", "down"))
+    out["C2 0.6B layer M=1"] = {**shape_entry(us, sum(layer_bytes(QWEN3_06B, 1).values())),
+                                "read_floor_us": round(floor_us, 3), "over_floor_us": round(us - floor_us, 3)}
     x = torch.randn((1, 1024), device=dev).to(torch.bfloat16)
     copies = [torch.randn((4096, 1024), device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(64)]
     ys = [torch.empty((1, 4096), device=dev, dtype=torch.bfloat16) for _ in range(64)]
     g = capture(lambda: [L.project(x, w, out=y) for w, y in zip(copies, ys)])
     us = time_graph(g) / 64
-    out["C1 0.6B qkv M=1 (no prologue)"] = shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096)
+    out["C1 0.6B qkv M=1 (no prologue)"] = floor_entry(shape_entry(us, 2 * 4096 * 1024 + 2 * 1024 + 2 * 4096),
+                                                       read_floor(copies))
     del model06, copies
     return out
 

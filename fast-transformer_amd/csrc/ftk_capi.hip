@@ -1,6 +1,7 @@
 // extern "C" entry points of libftk.so (declared in include/ftk.h): argument
 // checks, launch planning and dispatch to the gfx950 kernels.
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -510,7 +511,9 @@ static int attn_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t C, int64_t D, i
 // at its own address, until the process ends. Host code never passes the
 // array's name to a kernel (on the host it is only a stand-in for the symbol):
 // it passes the device address hipGetSymbolAddress returned for the current
-// device, looked up once per device and kept here.
+// device, looked up once per device and kept here. It starts zeroed (a device
+// variable without an initializer), as the argmax key words must be at a call's
+// start; every call leaves them zero.
 static __device__ __align__(256) unsigned char scratch[FTK_STATIC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
@@ -684,6 +687,16 @@ int ftk_plan_coverage(const ftk_plan* p, int64_t N, int epilogue, int32_t* count
   return FTK_OK;
 }
 
+// The one-launch greedy argmax is on unless FTK_ARGMAX_GATHER=0 (read once per process): the
+// switch keeps the two-launch form measurable beside it.
+static bool argmax_gather_on() {
+  static const bool on = [] {
+    const char* v = getenv("FTK_ARGMAX_GATHER");
+    return v == nullptr || strcmp(v, "0") != 0;
+  }();
+  return on;
+}
+
 static bool overlaps(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
   if (a == nullptr || b == nullptr) return false;
   const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
@@ -760,6 +773,12 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   if (p.kind == FTK_KIND_RING && r.residual != nullptr) return FTK_ERR_UNSUPPORTED;
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
+  // Greedy argmax in one launch (argmax_gather) for the STREAM kind: one row, or at most one key
+  // word per gathering lane. (M = 1 lm_head: 184.7-185.1 us per graph node against 189.0-190.8 with
+  // the second launch, same box. The RING kind at M = 5 measured the other way, 189.8-190.0 against
+  // 186.5-187.0, so its keys go to the second launch.)
+  a.fused = epilogue == FTK_EPI_ARGMAX && argmax_gather_on() && p.kind == FTK_KIND_STREAM &&
+            (M == 1 || p.grid <= p.threads);
   hipError_t e;
   if (p.kind == FTK_KIND_STREAM) {
     StreamShape g = {p.rows_per_wave, p.waves, p.grid, p.tiles};
@@ -785,7 +804,7 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
     m.row_scale = gamma != nullptr ? (const float*)(ws + kWsScale) : nullptr;
     e = launch_mfma(a, epilogue, shape, m, s);
   }
-  if (e == hipSuccess && epilogue == FTK_EPI_ARGMAX)
+  if (e == hipSuccess && epilogue == FTK_EPI_ARGMAX && !a.fused)
     e = launch_argmax_finalize(a.keys, p.grid, (int)M, ids, ids_bytes, top, s);
   return hip_status(e);
 }
@@ -1065,6 +1084,14 @@ int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride,
   a.dim = (int)dim;
   a.mode = mode;
   return hip_status(launch_qk_rope(a, (int)(batch * tokens), reinterpret_cast<hipStream_t>(stream)));
+}
+
+int ftk_stream_read(const void* src, int64_t bytes, void* sink, int grid, int loads, void* stream) {
+  if (!src || !sink || bytes < 16 || bytes % 16 != 0 || grid < 0 || !aligned16(src)) return FTK_ERR_INVALID;
+  if (loads != 2 && loads != 4 && loads != 8 && loads != 16) return FTK_ERR_INVALID;
+  if (grid == 0 && stream_read_once_grid(bytes, loads) > INT32_MAX) return FTK_ERR_INVALID;
+  return hip_status(launch_stream_read(src, bytes, (uint32_t*)sink, grid, loads,
+                                       reinterpret_cast<hipStream_t>(stream)));
 }
 
 int ftk_merge_splits_bf16(const float* partial, int64_t splits, int64_t count, void* out, void* stream) {

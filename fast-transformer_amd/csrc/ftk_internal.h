@@ -25,7 +25,8 @@ struct ProjArgs {
   void* ids;              // [M] int32 or int64
   int ids_bytes;
   float* top;             // [M] winning logit as FP32, or null
-  unsigned long long* keys;  // [grid][M] per-workgroup best keys (workspace)
+  unsigned long long* keys;  // [grid][M] per-workgroup best keys (workspace; zero between calls)
+  int fused;              // 1: one extra workgroup, the grid's last, gathers the keys (argmax_gather)
   // Prologue inputs beyond x (gamma != null only): the rows the norm reads are
   //   s[m] = bf16(xrow(m) + residual[m])   (or xrow(m) without a residual),
   // xrow(m) = x[x_ids[m]] (an embedding gather) or x[m]. Workgroup 0 stores s
@@ -46,6 +47,140 @@ __device__ __forceinline__ uint32_t store_bits(const ProjArgs& a, float s, int m
   const uint32_t b = f32_to_bf16(s);
   if (a.out_add == nullptr) return b;
   return f32_to_bf16(bf16_to_f32(b) + bf16_to_f32(a.out_add[(size_t)m * a.N + n]));
+}
+
+// ---- greedy argmax in one launch ------------------------------------------------
+// With a.fused, every tile workgroup publishes its best key per row, keys[wg M + m],
+// as an agent-scope store (coherent across the XCDs' L2s) of a non-zero word, and
+// one extra workgroup -- the grid's last, which walks no tiles -- gathers them: it
+// polls the words until each is non-zero, reduces them to the ids (and the top
+// values), and zeroes every word once it has read it. The key region is zero
+// before every call (zeroed at allocation; the two-launch finalize zeroes what it
+// reads too), so a non-zero word is a key of this call. A key is never zero: its
+// low half is ~index, and a workgroup without outputs publishes 1, below every
+// real key (whose high half is at least orderable(-inf) > 0).
+// Only the gatherer waits on other workgroups, so its wait ends in whatever order
+// the workgroups run (it holds one workgroup slot; the others need no more). The
+// wait is bounded all the same: past kGatherTicks of the 100 MHz clock the gather
+// stops and writes id -1 (top NaN) for the row.
+constexpr uint64_t kGatherTicks = 100000000ull;  // 1 s
+// Workgroups added to the walkers' grid: one per XCD, so that a grid that is a
+// multiple of 8 stays one (the hardware deals workgroups to the 8 XCDs in turn,
+// which the RING kind's per-XCD tile order relies on). The last gathers; the
+// others return at once.
+constexpr int kGatherExtra = 8;
+
+__device__ __forceinline__ void publish_key(const ProjArgs& a, size_t slot, unsigned long long k) {
+  if (a.fused)
+    __hip_atomic_store(a.keys + slot, k ? k : 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    a.keys[slot] = k;
+}
+
+__device__ __forceinline__ unsigned long long take_key(unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void clear_key(unsigned long long* p) {
+  __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void write_id(const ProjArgs& a, int m, unsigned long long k, bool late) {
+  const int64_t id = late ? -1 : (int64_t)key_index(k);
+  if (a.ids_bytes == 8)
+    reinterpret_cast<int64_t*>(a.ids)[m] = id;
+  else
+    reinterpret_cast<int32_t*>(a.ids)[m] = (int32_t)id;
+  if (a.top != nullptr) a.top[m] = late ? __uint_as_float(0x7FC00000u) : from_orderable((uint32_t)(k >> 32));
+}
+
+// The gathering workgroup (T threads) of a grid whose `walkers` tile workgroups
+// walk `tiles` tiles (walker w: tiles w, w + walkers, ..., so the first tiles %
+// walkers walkers take one tile more). It first waits, with one lane and short
+// sleeps, for the last word of the last walker with the most tiles: the walkers
+// start in order, so by then the others are nearly all done, and a gatherer that
+// starts early does not load the memory system while they stream. Then every
+// word is read in one of two
+// layouts: one row (thread t reads words t, t + T, ..., eight at a time) or at
+// most T walkers (thread t reads word t of each of the M <= MR rows at once).
+// Loads are issued together and then checked; a word that is still zero is read
+// again after a short sleep. `red` is the kernel's own LDS, T / 64 * MR words
+// (the workgroup walks no tiles, so nothing else uses it).
+template <int T, int MR>
+__device__ void argmax_gather(const ProjArgs& a, int walkers, int tiles, unsigned long long* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = a.M;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  if (tid == 0) {
+    const int longest = (tiles % walkers ? tiles % walkers : walkers) - 1;
+    unsigned long long* last = a.keys + (size_t)longest * M + M - 1;
+    while (take_key(last) == 0ull && __builtin_amdgcn_s_memrealtime() - t0 <= kGatherTicks)
+      __builtin_amdgcn_s_sleep(8);
+  }
+  __syncthreads();
+  bool late = false;
+  unsigned long long best[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) best[m] = 0ull;
+  if (M == 1) {
+    for (int base = tid; base < walkers && !late; base += 8 * T) {
+      uint32_t need = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (base + u * T < walkers) need |= 1u << u;
+      while (need) {
+        unsigned long long k[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) k[u] = take_key(a.keys + min(base + u * T, walkers - 1));
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (((need >> u) & 1u) && k[u] != 0ull) {
+            best[0] = key_max(best[0], k[u]);
+            need &= ~(1u << u);
+            clear_key(a.keys + base + u * T);
+          }
+        if (need) {
+          if (__builtin_amdgcn_s_memrealtime() - t0 > kGatherTicks) {
+            late = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
+        }
+      }
+    }
+  } else if (tid < walkers) {
+    uint32_t need = (1u << M) - 1u;  // M <= MR <= 16
+    while (need) {
+      unsigned long long k[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) k[m] = m < M ? take_key(a.keys + (size_t)tid * M + m) : 0ull;  // M: uniform
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (((need >> m) & 1u) && k[m] != 0ull) {
+          best[m] = key_max(best[m], k[m]);
+          need &= ~(1u << m);
+          clear_key(a.keys + (size_t)tid * M + m);
+        }
+      if (need) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kGatherTicks) {
+          late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) best[m] = wave_max_key(best[m]);
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[wave * MR + m] = best[m];
+  }
+  const bool any_late = __syncthreads_or(late) != 0;
+  if (tid < M) {
+    unsigned long long k = red[tid];
+    for (int w = 1; w < T / 64; ++w) k = key_max(k, red[w * MR + tid]);
+    write_id(a, tid, k, any_late);
+  }
 }
 
 // Row m of the prologue's x: x[x_ids[m]] (embedding gather) or x[m]. The host
@@ -221,7 +356,7 @@ struct RopeArgs {
 hipError_t launch_qk_rope(const RopeArgs& a, int rows, hipStream_t stream);
 
 // Greedy-argmax second stage: ids[m] (and top[m]) from keys[slot * M + m], slot < slots.
-hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
+hipError_t launch_argmax_finalize(unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream);
 
 // Ragged or unaligned shapes: one wave per weight row, scalar loads, no prologue/epilogue.
@@ -242,5 +377,11 @@ hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids,
                          unsigned long long* keys, hipStream_t stream);
 int argmax_blocks(int vocab);
 hipError_t launch_merge_splits(const float* partial, int splits, int64_t count, uint16_t* out, hipStream_t stream);
+// Pure streaming read of `bytes` (the bandwidth reference of the projections): `grid`
+// persistent workgroups, or with grid 0 one-shot workgroups of `loads` chunks per lane;
+// `loads` (2, 4, 8 or 16) 16-byte loads in flight per lane.
+hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int grid, int loads,
+                              hipStream_t stream);
+int64_t stream_read_once_grid(int64_t bytes, int loads);
 
 }  // namespace ftk

@@ -401,9 +401,11 @@ __global__ __launch_bounds__(kThreads) void argmax_block_rows_kernel(const uint1
 // the id (and the winning logit) (argmax.py:34-48 _first_best). The keys were
 // just written by other CUs, so every load is a long trip: each thread issues
 // its kFinalizeLoads loads together, and 1024 threads cover 8192 slots a round.
+// Every key is zeroed once read: the key region is zero between calls, which the
+// one-launch argmax (argmax_gather) relies on when it shares the workspace.
 constexpr int kFinalizeThreads = 1024;
 constexpr int kFinalizeLoads = 8;
-__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const unsigned long long* __restrict__ keys,
+__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(unsigned long long* __restrict__ keys,
                                                                            int slots, int rows, void* ids,
                                                                            int ids_bytes, float* top) {
   __shared__ unsigned long long red[kFinalizeThreads / 64];
@@ -416,6 +418,11 @@ __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const
     for (int u = 0; u < kFinalizeLoads; ++u) {
       const int s = base + u * kFinalizeThreads + tid;
       k[u] = s < slots ? keys[(size_t)s * rows + row] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < kFinalizeLoads; ++u) {
+      const int s = base + u * kFinalizeThreads + tid;
+      if (s < slots) keys[(size_t)s * rows + row] = 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kFinalizeLoads; ++u) best = key_max(best, k[u]);
@@ -543,7 +550,7 @@ hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids,
   return launch_argmax_finalize(keys, blocks, rows, ids, ids_bytes, top, stream);
 }
 
-hipError_t launch_argmax_finalize(const unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
+hipError_t launch_argmax_finalize(unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream) {
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(kFinalizeThreads), 0, stream, keys, slots, M, ids,
                      ids_bytes, top);

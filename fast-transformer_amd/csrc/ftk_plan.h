@@ -219,9 +219,10 @@ FTK_HD constexpr int ring_max_depth(int c, int kw, int d, int nx, bool pro, int 
 }
 
 // ---- workspace layout of one projection call (bytes) -----------------------
-// Nothing in it carries state between calls: every slot a kernel reads was
-// written earlier in the same call (row scales by the prologue pass, argmax
-// keys by every workgroup), so no zeroing or clearing protocol is needed.
+// The row scales are written by the prologue pass before they are read. The
+// argmax key words are zero between calls: a workspace is zeroed when it is
+// allocated, and whichever reads the keys (the finalize launch, or the gathering
+// workgroup of the one-launch argmax) zeroes each word it has read.
 constexpr int64_t kWsScale = 0;     // [32] f32 RMSNorm row scales (MFMA kind)
 constexpr int64_t kWsKeys = 256;    // [grid][M] u64 per-workgroup greedy-argmax keys
 

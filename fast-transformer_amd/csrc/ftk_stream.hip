@@ -45,6 +45,16 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   const int M = a.M;  // <= MR
   const int outputs = gemv_outputs(EPI, a.N);
   const size_t first = (size_t)(kw * 64 + lane) * 8;  // this lane's chunk j = 0
+  int walkers = (int)gridDim.x;  // workgroups walking tiles
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (a.fused) {
+      walkers -= kGatherExtra;
+      if ((int)blockIdx.x >= walkers) {  // the extra workgroups walk no tiles; the last gathers
+        if ((int)blockIdx.x == walkers + kGatherExtra - 1) argmax_gather<T, MR>(a, walkers, tiles, &best_lds[0][0]);
+        return;
+      }
+    }
+  }
 
   auto row_ptrs = [&](int tile, const uint16_t* (&wr)[RPW]) {
 #pragma unroll
@@ -133,7 +143,7 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   // ---- tiles: consume, prefetch the next tile chunk by chunk, park the totals
   int count = 0;
   for (;;) {
-    const int next = tile + (int)gridDim.x;
+    const int next = tile + walkers;
     float acc[RPW][MR];
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     const int p = e % PW;
     const int g = (e / PW) % GROUPS;
     const int i = e / (PW * GROUPS);
-    const int col = gemv_output(wg + i * (int)gridDim.x, g, p, PW, GROUPS);
+    const int col = gemv_output(wg + i * walkers, g, p, PW, GROUPS);
     if (col >= outputs) continue;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -206,7 +216,8 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   }
 
   if constexpr (EPI == EPI_ARGMAX) {
-    // This workgroup's best key per input row; the finalize pass reduces the workgroups.
+    // This workgroup's best key per input row; the finalize pass (or the gathering
+    // workgroup) reduces the workgroups.
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       best[m] = wave_max_key(best[m]);
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     if (tid < M) {
       unsigned long long k = best_lds[0][tid];
       for (int w = 1; w < W; ++w) k = key_max(k, best_lds[w][tid]);
-      a.keys[(size_t)blockIdx.x * M + tid] = k;
+      publish_key(a, (size_t)blockIdx.x * M + tid, k);
     }
   }
 }
@@ -302,7 +313,9 @@ hipError_t launch_stream(const ProjArgs& a, int epi, const StreamShape& s, hipSt
   // Every workgroup walks at most kStreamMaxTiles tiles (their totals wait in LDS).
   if (s.grid < 1 || s.grid > s.tiles || (s.tiles + s.grid - 1) / s.grid > kStreamMaxTiles)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k, dim3(s.grid), dim3(64 * stream_waves(s.kw)), 0, stream, a, s.tiles);
+  // With the one-launch argmax, kGatherExtra more workgroups than the walkers: the last gathers the keys.
+  const int grid = s.grid + (epi == EPI_ARGMAX && a.fused ? kGatherExtra : 0);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(64 * stream_waves(s.kw)), 0, stream, a, s.tiles);
   return hipGetLastError();
 }
 

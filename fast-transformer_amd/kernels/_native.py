@@ -119,6 +119,7 @@ SIGNATURES = {
                                       _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "ftk_plan_project": (_int, [_i64, _i64, _i64, _int, _int, ctypes.POINTER(Config), ctypes.POINTER(Plan)]),
+    "ftk_stream_read": (_int, [_c_void_p, _i64, _c_void_p, _int, _int, _c_void_p]),
     "ftk_plan_coverage": (_int, [ctypes.POINTER(Plan), _i64, _int, ctypes.POINTER(ctypes.c_int32), _i64,
                                  ctypes.POINTER(_i64)]),
 }
@@ -190,12 +191,13 @@ _RETIRED = []
 
 
 def workspace(device, need, purpose):
-    """Per-device, per-purpose scratch buffer of at least ``need`` bytes.
+    """Per-device, per-purpose scratch buffer of at least ``need`` bytes, zeroed when allocated.
 
-    The kernels keep only per-call scratch there (per-workgroup argmax keys,
-    RMSNorm row scales), written before it is read in the same call, so no
-    initial contents are needed. A buffer only grows, outside graph capture;
-    a replaced buffer is kept alive for graphs that captured its address.
+    The kernels keep per-call scratch there (RMSNorm row scales, per-workgroup
+    argmax keys). The argmax key words must be zero when a call starts; every
+    call leaves the words it used zero again. A buffer only grows, outside
+    graph capture; a replaced buffer is kept alive for graphs that captured its
+    address.
     """
     key = (device, purpose)
     ws = _WORKSPACES.get(key)

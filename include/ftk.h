@@ -19,11 +19,17 @@
  *     code other than FTK_OK or FTK_ERR_HIP is returned.
  *   - M (rows of x) is 1..FTK_MAX_ROWS, as the reference's MAX_ROWS = 32
  *     (engine/kernels/linear.py:343); larger M is the caller's native GEMM.
- *   - Workspaces hold per-call scratch only (per-workgroup argmax keys,
- *     RMSNorm row scales): no initial contents are required and nothing carries
- *     over between calls. Calls that share a workspace must not run
- *     concurrently. No kernel waits on another workgroup: they use no
- *     device-scope fences or tickets.
+ *   - Workspaces hold per-call scratch (RMSNorm row scales, per-workgroup
+ *     argmax keys). Zero a workspace once when it is allocated: the argmax key
+ *     words (from byte 256) must be zero when a call starts, and every call
+ *     leaves the ones it used zero again (the one-launch argmax reads a
+ *     non-zero word as a key of the current call). Nothing else carries over
+ *     between calls. Calls that share a workspace must not run concurrently.
+ *   - No kernel uses device-scope fences or tickets. One workgroup waits on
+ *     others: the extra, last workgroup of a one-launch lm_head + argmax (the
+ *     STREAM kind, M = 1) reads the other workgroups' key words, with a
+ *     bounded wait (1 s; then the row's id is -1). The others never wait, so
+ *     its wait ends in whatever order the workgroups run.
  */
 #ifndef FTK_H
 #define FTK_H
@@ -171,8 +177,10 @@ int ftk_lm_head_argmax_bf16(const void* x, const void* gamma, float eps, const v
  * graph capture that may not call hipMalloc, tight serving loops, harnesses that forbid
  * allocation. No counterpart in the reference. It takes no workspace and allocates nothing:
  * the per-workgroup argmax keys live in a static device array of FTK_STATIC_SCRATCH_BYTES
- * (1 MiB) that every GPU the library runs on holds until the process ends. Results are those of
- * ftk_lm_head_argmax_bf16 bit for bit (same kernels). A call that needs more keys than the array
+ * (1 MiB) that every GPU the library runs on holds until the process ends. The array starts
+ * zeroed and every call leaves its key words zero, as the workspace convention above asks.
+ * Results are those of ftk_lm_head_argmax_bf16 bit for bit (same kernels). A call that needs
+ * more keys than the array
  * holds (e.g. 32 rows of a 151936-entry vocabulary) returns FTK_ERR_TOO_LARGE and launches nothing.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
  * threads) race and give wrong ids; keep them in one stream. */
@@ -353,6 +361,18 @@ int ftk_qk_rope_cache_bf16(const void* packed, int splits, int64_t split_stride,
                            int64_t table_rows, const int64_t* position, const int64_t* phases, void* query,
                            void* keys, void* values, int64_t batch, int64_t tokens, int64_t q_heads,
                            int64_t kv_heads, int64_t capacity, int64_t dim, int mode, void* stream);
+/* ---- measurement --------------------------------------------------------------- */
+/* A pure streaming read of `bytes` (a multiple of 16, src 16-byte aligned) with the
+ * projection kernels' load path: `grid` persistent workgroups of 256 lanes with a
+ * rolling window of `loads` (2, 4, 8 or 16) 16-byte non-temporal loads per lane, or,
+ * with grid 0, one-shot workgroups that each read 256 `loads` chunks (ceil(bytes /
+ * (4096 loads)) of them) and exit; nothing computed but an XOR fold. sink: one
+ * 32-bit word per workgroup, practically never written. Its time is the floor
+ * a projection reading the same bytes in one launch is measured against (the
+ * bandwidth reference of bench.py). No counterpart in the reference, which prices
+ * its kernels against the nominal bandwidth only (agent/EXPERIMENTS.md:2231-2239). */
+int ftk_stream_read(const void* src, int64_t bytes, void* sink, int grid, int loads, void* stream);
+
 /* ---- planning (host only, no device needed) ---------------------------------- */
 /* The launch ftk_decode_attention_bf16 would make on `compute_units` CUs. */
 int ftk_plan_decode_attention(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t capacity, int64_t dim,

@@ -105,3 +105,24 @@ def test_merge_splits(cuda):
     partial = torch.randn(4, 3, 1000, device=cuda) * 100
     got = M.materialize(M.Split(partial, (3, 1000)))
     assert np.array_equal(to_bits(got), path.merge_splits(partial.cpu().numpy()))
+
+
+@pytest.mark.parametrize("grid,loads", [(1, 2), (7, 4), (256, 8), (2048, 16), (0, 2), (0, 4), (0, 16)])
+def test_stream_read_reads_every_chunk_into_its_owner(cuda, grid, loads):
+    """The bandwidth reference (ftk_stream_read) really reads the bytes: a buffer of zeros with one
+    chunk equal to the kernel's store constant makes exactly the workgroup that owns that chunk store
+    the constant into its sink word. Persistent form: chunk c belongs to workgroup (c mod 256 grid) //
+    256; one-shot form (grid 0): to workgroup c // (256 loads)."""
+    from kernels import _native
+    chunks = 3 * 256 * max(grid, 5) + 77              # a partial last round
+    for c in (0, chunks // 2 + 3, chunks - 2):        # not the last chunk: it is re-read past the end
+        buf = torch.zeros(chunks * 4, dtype=torch.int32, device=cuda)
+        buf[4 * c] = int(np.int32(np.uint32(0x9E3779B9)))
+        words = grid if grid else -(-chunks // (256 * loads))
+        sink = torch.zeros(words, dtype=torch.int32, device=cuda)
+        _native.call("ftk_stream_read", _native.ptr(buf), chunks * 16, _native.ptr(sink), grid, loads,
+                     _native.stream_of(buf))
+        torch.cuda.synchronize()
+        want = np.zeros(words, dtype=np.uint32)
+        want[(c % (256 * grid)) // 256 if grid else c // (256 * loads)] = 0x9E3779B9
+        np.testing.assert_array_equal(sink.cpu().numpy().view(np.uint32), want)

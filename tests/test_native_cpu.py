@@ -126,6 +126,12 @@ def test_invalid_arguments_rejected_before_any_launch():
         assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64,
                                          64, 0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
     assert lib.ftk_embed_rms_norm_bf16(fake, 3, fake, fake, fake, fake, 1, 8, 1e-6, None) == _native.FTK_ERR_INVALID
+    # the streaming-read reference: whole 16-byte chunks, an aligned source, a sink, a built window
+    assert lib.ftk_stream_read(fake, 24, fake, 1, 4, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_stream_read(ctypes.c_void_p(18), 32, fake, 1, 4, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_stream_read(fake, 32, None, 1, 4, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_stream_read(fake, 32, fake, -1, 4, None) == _native.FTK_ERR_INVALID
+    assert lib.ftk_stream_read(fake, 32, fake, 1, 3, None) == _native.FTK_ERR_INVALID
 
 
 @pytest.mark.parametrize("m", [0, 33])
