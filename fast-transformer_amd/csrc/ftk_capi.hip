@@ -76,6 +76,16 @@ struct StreamDefault {
 };
 static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
   if (M < 1 || M > kStreamMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0};
+  // One wave per row group (KW = 1: whole rows per wave, no LDS round and no barrier
+  // before the stores) for rows of at most 3072 elements at one x row, STORE and
+  // SwiGLU. Qwen3-0.6B shapes, graphs of 28-64 distinct weights: 0.6B QKV without
+  // the norm 3.52 -> 3.30 us, with it 3.87 -> 3.74, O 3.06 -> 2.96, gate/up + SwiGLU
+  // 4.51 -> 4.46, down 3.47 -> 3.28. At the 8B shapes it measured slower (QKV
+  // 9.45 -> 9.58 us, O 7.04 -> 7.12, gate/up 29.7 -> 31.0).
+  if (M == 1 && K <= 3072 && epi != FTK_EPI_ARGMAX) {
+    const int rpw = (K <= 1024 || epi == FTK_EPI_SWIGLU) ? 2 : 1;
+    if (stream_supported(1, rpw, (int)K, 1, epi)) return {rpw, 1};
+  }
   // Rows longer than 8192 (down, K = 12288) split K over 8 waves (M = 1 down:
   // 16.25 us against 17.0 with 4); otherwise 4 waves first.
   const int order_long[] = {8, 4, 2, 1}, order[] = {4, 2, 1, 8};
@@ -98,7 +108,10 @@ static StreamDefault stream_default(int64_t M, int epi, int64_t N, int64_t K) {
 // per workgroup when a prologue is paid per workgroup (0.6B gate/up + SwiGLU:
 // 4.70 -> 4.45 us), one without it (0.6B QKV without the norm: 3.60 -> 3.48 us,
 // graphs of 64 distinct weights).
-static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K, bool pro) {
+static int64_t stream_default_cap(int tiles, int cus, int64_t M, int64_t K, bool pro, int kw) {
+  // One wave per row group at one x row: one tile per workgroup, two with the
+  // prologue (each wave forms its row's norm scale once per workgroup).
+  if (kw == 1 && M == 1) return pro ? (tiles + 1) / 2 : tiles;
   if (K <= 1024 && tiles <= 4096) {
     if (!pro) return tiles;
     return tiles / 2 > 2LL * cus ? tiles / 2 : 2LL * cus;
@@ -329,7 +342,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // Fewest workgroups that keep every walk at the same depth, and no deeper than
     // kStreamMaxTiles (each workgroup parks its tiles' wave totals in LDS).
     const int64_t cap = cfg && cfg->groups_per_cu ? (int64_t)cfg->groups_per_cu * cus
-                                                  : stream_default_cap(p->tiles, cus, M, K, pro);
+                                                  : stream_default_cap(p->tiles, cus, M, K, pro, kw);
     const int64_t floor = (p->tiles + kStreamMaxTiles - 1) / kStreamMaxTiles;
     const int64_t units = cap > floor ? cap : floor;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));

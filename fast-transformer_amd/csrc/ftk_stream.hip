@@ -97,7 +97,31 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     for (int r = 0; r < RPW; ++r) wv[j][r] = load_stream16(wr[r] + j * kStep);
 
   // ---- RMSNorm prologue: normalise the slice in registers -------------------
-  if constexpr (PRO) {
+  if constexpr (PRO && KW == 1) {
+    // One wave per row group holds every chunk of the row: lane l's chunk j is
+    // j 64 + l. The other kinds' thread t < 256 sums chunks t, t + 256, ..., i.e.
+    // wave w's lane l sums chunks j = w, w + 4, ... of this lane. So each wave
+    // forms those four per-wave sums itself, in that order, reduces each with the
+    // same DPP tree and adds them in wave order: the same scale bits, no barrier.
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float parts[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = w; j < C; j += kWaves) ss = sum_squares8(xr[m][j], ss);
+        parts[w] = wave_sum(ss);
+      }
+      if (a.sum != nullptr && blockIdx.x == 0 && wave == 0 && m < M) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) store16(a.sum + (size_t)m * K + first + j * kStep, xr[m][j]);
+      }
+      const float scale = rms_scale(parts, K, a.eps);
+#pragma unroll
+      for (int j = 0; j < C; ++j) xr[m][j] = norm8(xr[m][j], g[j], scale);
+    }
+  } else if constexpr (PRO) {
     // Sum of squares in the thread order of the other kinds' prologues
     // (thread t < 256: chunks t, t + 256, ...), so every kind scales a row
     // alike. With KW = W = 4 thread t's own chunks (4 j + wave) 64 + lane are
@@ -170,17 +194,37 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
 #pragma unroll
           for (int m = 0; m < MR; ++m) acc[r][m] = dot8(wv[j][r], xr[m][j], acc[r][m]);
     }
+    if constexpr (KW == 1 && EPI != EPI_ARGMAX) {
+      // The wave holds its rows' whole sums: it finishes its outputs now, with no
+      // LDS round and no barrier (lane 0 stores; the sums are wave-uniform).
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
+      for (int p = 0; p < PW; ++p) {
+        const int col = gemv_output(tile, grp, p, PW, GROUPS);
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float t = wave_sum(acc[r][m]);
-        if (lane == 0) part[count][wave][r][m] = t;
+        for (int m = 0; m < MR; ++m) {
+          const float s = wave_sum(acc[p][m]);
+          if constexpr (EPI == EPI_STORE) {
+            if (lane == 0 && m < M && col < outputs) a.y[(size_t)m * a.N + col] = (uint16_t)store_bits(a, s, m, col);
+          } else {
+            const float u = wave_sum(acc[PW + p][m]);
+            if (lane == 0 && m < M && col < outputs) a.y[(size_t)m * (a.N / 2) + col] = (uint16_t)swiglu_bf16(s, u);
+          }
+        }
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float t = wave_sum(acc[r][m]);
+          if (lane == 0) part[count][wave][r][m] = t;
+        }
+    }
     ++count;
     if (next >= tiles) break;
     tile = next;
   }
+  if constexpr (KW == 1 && EPI != EPI_ARGMAX) return;  // every output is stored
   __syncthreads();
 
   // ---- epilogue: every thread takes outputs (tile i, group, slot) ------------
@@ -260,6 +304,20 @@ typedef void (*StreamKernel)(ProjArgs, int);
   FTK_STREAM_SHAPE(8, 2, 3, 8, PRO, EPI) \
   FTK_STREAM_SHAPE(8, 4, 3, 8, PRO, EPI)
 
+// One wave per row group (KW = 1, whole rows per wave, no barrier in the
+// epilogue) at one x row: the K of the Qwen3 shapes up to 4096. One row per wave
+// only where there is no SwiGLU (which pairs a gate and an up row).
+#define FTK_STREAM_SHAPES_KW1(PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 2, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 4, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 6, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 8, 1, PRO, EPI)
+#define FTK_STREAM_SHAPES_KW1_ROW(PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 2, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 4, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 6, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 8, 1, PRO, EPI)
+
 #define FTK_STREAM_SHAPE(MR, R, CC, KW, PRO, EPI) \
   if (rpw == R && c == CC && kw == KW) return stream_kernel<MR, R, CC, KW, (KW > kWaves ? KW : kWaves), PRO, EPI>;
 
@@ -269,6 +327,12 @@ static StreamKernel pick_stream_shape(int rpw, int c, int kw) {
     FTK_STREAM_SHAPES_8(PRO, EPI)
   } else {
     FTK_STREAM_SHAPES(MR, PRO, EPI)
+  }
+  if constexpr (MR == 1) {
+    FTK_STREAM_SHAPES_KW1(PRO, EPI)
+    if constexpr (EPI != EPI_SWIGLU) {
+      FTK_STREAM_SHAPES_KW1_ROW(PRO, EPI)
+    }
   }
   return nullptr;
 }

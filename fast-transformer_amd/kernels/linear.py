@@ -270,7 +270,7 @@ def _candidates(m, n, k, epilogue=_native.EPI_STORE, prologue=False):
         for rpw, unroll, kw in ((2, 4, 1), (4, 2, 1), (2, 2, 2), (2, 4, 2), (1, 1, 4), (2, 2, 4)):
             configs.append((_native.KIND_GEMV, rpw, unroll, 8, kw))
     if m <= 8:
-        for rpw in (2, 4, 8):
+        for rpw in (1, 2, 4, 8):
             for kw in (1, 2, 4, 8):
                 for gpc in (2, 16, 32):
                     configs.append((_native.KIND_STREAM, rpw, 0, gpc, kw))

@@ -158,3 +158,69 @@ def test_argmax_ties_take_lowest_index(cuda):
 def test_default_plan_is_stream_for_model_shapes(cuda):
     for n, k in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288), (4096, 1024), (1024, 2048), (1024, 3072)):
         assert L.plan(1, n, k).kind == _native.KIND_STREAM, (n, k)
+
+
+#: One wave per row group (KW = 1) at one x row: whole rows per wave, no LDS round or barrier in the
+#: STORE / SwiGLU epilogue (rows per wave, chunks per lane C; K = 512 C).
+STREAM_SHAPES_KW1 = ((1, 2), (2, 2), (1, 4), (2, 4), (1, 6), (2, 6), (1, 8), (2, 8))
+
+
+@pytest.mark.parametrize("rpw,c", STREAM_SHAPES_KW1)
+@pytest.mark.parametrize("gpc", [0, 1])
+def test_one_wave_per_row_group_equals_gemv_kind_and_oracle(cuda, rpw, c, gpc):
+    """KW = 1: every epilogue, with and without the prologue (whose sum of squares each wave forms in
+    the other kinds' thread order), bit for bit as the GEMV kind with KW = 1, within the bar of the
+    oracle; the planner's grid (gpc 0) or one workgroup per CU walking 4..8 tiles (gpc 1)."""
+    k = 512 * c
+    n = 8000 + 4 * rpw + 3  # ragged last tile
+    x, w, g = _inputs(1, n, k, seed=800 + rpw + 10 * c, device=cuda)
+    cfg = stream(rpw, 1, gpc)
+    assert L.plan(1, n, k, _native.EPI_STORE, config=cfg).kind == _native.KIND_STREAM
+    got = L.project(x, w, cfg)
+    assert torch.equal(got, L.project(x, w, gemv(1)))
+    assert within(to_bits(got), path.project(to_bits(x), to_bits(w)))
+    normed = L.rms_norm_linear(x, g, 1e-6, w, config=cfg)
+    assert torch.equal(normed, L.rms_norm_linear(x, g, 1e-6, w, config=gemv(1)))
+    assert within(to_bits(normed), path.norm_project(to_bits(x), to_bits(g), 1e-6, to_bits(w)))
+    # the norm's scale is the other kinds' bit for bit: the standalone norm, then the plain call
+    from kernels.rmsnorm import rms_norm
+    assert torch.equal(normed, L.project(rms_norm(x, g, 1e-6), w, cfg))
+    # residual prologue: the stored sum and the projection
+    r = seeded((1, k), seed=801, device=cuda)
+    y_r, s_r = L.add_rms_norm_linear(x, r, g, 1e-6, w, config=cfg)
+    y_g, s_g = L.add_rms_norm_linear(x, r, g, 1e-6, w, config=gemv(1))
+    assert torch.equal(y_r, y_g) and torch.equal(s_r, s_g)
+    if rpw % 2 == 0:
+        for gain in (None, g):
+            sw = S.gate_up_swiglu(x, w[: 2 * (n // 2)], gain, 1e-6, config=cfg)
+            assert torch.equal(sw, S.gate_up_swiglu(x, w[: 2 * (n // 2)], gain, 1e-6, config=gemv(1)))
+    ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=cfg)
+    ids_g, logits_g = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=gemv(1))
+    assert torch.equal(logits, logits_g) and torch.equal(ids, ids_g)
+    np.testing.assert_array_equal(ids.cpu().numpy(), path.argmax_first(to_bits(logits)))
+
+
+@pytest.mark.parametrize("n,k,epi,pro", [(4096, 1024, 0, False), (4096, 1024, 0, True), (6144, 1024, 1, True),
+                                         (1024, 2048, 0, False), (1024, 3072, 0, False), (6144, 4096, 0, True),
+                                         (4096, 4096, 0, False), (24576, 4096, 1, True)])
+def test_one_wave_per_row_group_at_model_shapes(cuda, n, k, epi, pro):
+    """The Qwen3 0.6B / 8B M = 1 shapes on KW = 1 against the oracle (and against the planner's
+    default launch within one BF16 ulp, two after SwiGLU's second rounding: the K split differs, so
+    the FP32 sums are ordered differently)."""
+    x, w, g = _inputs(1, n, k, seed=900 + n % 97 + k % 89, device=cuda)
+    cfg = stream(2, 1)
+    if epi == _native.EPI_SWIGLU:
+        got = S.gate_up_swiglu(x, w, g if pro else None, 1e-6, config=cfg)
+        want = path.gate_up_swiglu(to_bits(x), to_bits(w), to_bits(g) if pro else None, 1e-6)
+        base = S.gate_up_swiglu(x, w, g if pro else None, 1e-6)
+    elif pro:
+        got = L.rms_norm_linear(x, g, 1e-6, w, config=cfg)
+        want = path.norm_project(to_bits(x), to_bits(g), 1e-6, to_bits(w))
+        base = L.rms_norm_linear(x, g, 1e-6, w)
+    else:
+        got = L.project(x, w, cfg)
+        want = path.project(to_bits(x), to_bits(w))
+        base = L.project(x, w)
+    assert within(to_bits(got), want)
+    diff = np.abs(to_bits(got).astype(np.int32) - to_bits(base).astype(np.int32))
+    assert diff.max() <= (2 if epi == _native.EPI_SWIGLU else 1)

@@ -368,11 +368,20 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
-    # rows of <= 1024 elements: one tile per workgroup without the norm (C1), two with it (C2)
+    # rows of <= 3072 elements at one x row: one wave per row group (KW = 1), one tile per workgroup
+    # without the norm (C1), two with it (C2); two rows per wave at K = 1024, one at 2048 and 3072
     _native.call("ftk_plan_project", 1, 4096, 1024, 0, 256, None, p)
-    assert p.kind == _native.KIND_STREAM and p.grid == p.tiles == 1024
+    assert p.kind == _native.KIND_STREAM and p.waves == 1 and p.rows_per_wave == 2 and p.grid == p.tiles == 512
     _native.call("ftk_plan_project", 1, 4096, 1024, _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_STREAM and p.grid == 512 and p.tiles == 1024
+    assert p.kind == _native.KIND_STREAM and p.waves == 1 and p.grid == 256 and p.tiles == 512
+    _native.call("ftk_plan_project", 1, 1024, 3072, 0, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.waves == 1 and p.rows_per_wave == 1 and p.grid == p.tiles == 256
+    _native.call("ftk_plan_project", 1, 6144, 1024, _native.EPI_SWIGLU | _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STREAM and p.waves == 1 and p.rows_per_wave == 2 and p.grid == 384
+    _native.call("ftk_plan_project", 1, 151936, 1024, _native.EPI_ARGMAX, 256, None, p)  # argmax: unchanged
+    assert p.kind == _native.KIND_STREAM and p.waves != 1
+    _native.call("ftk_plan_project", 1, 4096, 4096, 0, 256, None, p)  # the 8B shapes keep KW = 4
+    assert p.waves == 4
     # 5..16 rows: weight and x segments loaded straight into LDS (RING), one workgroup per CU
     _native.call("ftk_plan_project", 5, 4096, 4096, 0, 256, None, p)
     assert p.kind == _native.KIND_RING and p.threads == 512 and p.unroll == 2 and p.grid == 256
