@@ -78,7 +78,8 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int j = 0; j < C; ++j) xr[m][j] = m < M ? x_in(m, first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int j = 0; j < C; ++j)  // row 0 is always real (M >= 1): no branch around its loads
+      xr[m][j] = (m == 0 || m < M) ? x_in(m, first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
   u32x4_t g[PRO ? C : 1];
   if constexpr (PRO) {
 #pragma unroll
