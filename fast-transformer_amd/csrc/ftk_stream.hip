@@ -66,10 +66,13 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     }
   };
 
-  // ---- this lane's slice of x (and of the gain): small, mostly cache hits ---
-  // Issued first: loads complete in issue order, so the prologue below waits
-  // for these and not for the weight batch issued after them.
-  // With the prologue, row m is x[m] or the gathered x[x_ids[m]], plus the residual.
+  // ---- this lane's slice of x (and of the residual and the gain) ------------
+  // Small, mostly cache hits, issued first: loads complete in issue order, so
+  // the prologue below waits for these and not for the weight batch issued
+  // after them. Nothing is computed from a load before the weights are in
+  // flight: the residual add waits until then (an add at the load would be a
+  // join behind a runtime branch, and the join waits for the load). With the
+  // prologue, row m is x[m] or the gathered x[x_ids[m]], plus the residual.
   const uint16_t* xrow[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) xrow[m] = (PRO && m < M) ? x_row(a, m) : a.x + (size_t)m * K;
@@ -79,7 +82,18 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int j = 0; j < C; ++j)  // row 0 is always real (M >= 1): no branch around its loads
-      xr[m][j] = (m == 0 || m < M) ? x_in(m, first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
+      xr[m][j] = (m == 0 || m < M) ? load16(xrow[m] + first + j * kStep) : u32x4_t{0u, 0u, 0u, 0u};
+  const bool residual = PRO && a.residual != nullptr;
+  u32x4_t rr[PRO ? MR : 1][PRO ? C : 1];
+  if constexpr (PRO) {
+    if (residual) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+          if (m == 0 || m < M) rr[m][j] = load16(a.residual + (size_t)m * K + first + j * kStep);
+    }
+  }
   u32x4_t g[PRO ? C : 1];
   if constexpr (PRO) {
 #pragma unroll
@@ -96,6 +110,15 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   for (int j = 0; j < C; ++j)
 #pragma unroll
     for (int r = 0; r < RPW; ++r) wv[j][r] = load_stream16(wr[r] + j * kStep);
+  if constexpr (PRO) {
+    if (residual) {  // s = bf16(x + residual), as prologue_in forms it
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+          if (m == 0 || m < M) xr[m][j] = add8(xr[m][j], rr[m][j]);
+    }
+  }
 
   // ---- RMSNorm prologue: normalise the slice in registers -------------------
   if constexpr (PRO && KW == 1) {
