@@ -237,11 +237,29 @@ __device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsi
   return a > b ? a : b;
 }
 
-// Largest key of the wave, in every lane.
+// Largest 32-bit word of the wave, in every lane: the wave_sum lane pattern with
+// max (a masked-off row reads 0, the identity).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1, 0xF>(v));
+  v = max(v, dpp_u32<0x4E, 0xF>(v));
+  v = max(v, dpp_u32<0x141, 0xF>(v));
+  v = max(v, dpp_u32<0x140, 0xF>(v));
+  v = max(v, dpp_u32<0x142, 0xA>(v));
+  v = max(v, dpp_u32<0x143, 0xC>(v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Largest key of the wave, in every lane: the largest high word, then the largest
+// low word among the lanes that hold it (two DPP reductions instead of six
+// 64-bit lane shuffles through LDS).
 __device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) k = key_max(k, __shfl_xor(k, off));
-  return k;
+  const uint32_t hi = wave_max_u32((uint32_t)(k >> 32));
+  const uint32_t lo = wave_max_u32((uint32_t)(k >> 32) == hi ? (uint32_t)k : 0u);
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
 }
 
 __device__ __forceinline__ float silu_f32(float g) {

@@ -252,11 +252,15 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
   __syncthreads();
 
   // ---- epilogue: every thread takes outputs (tile i, group, slot) ------------
+  // The argmax keeps one wave when every output of the walk fits it: that wave
+  // alone reduces the keys, so no second barrier (the others leave now).
+  constexpr bool kOneWave = EPI == EPI_ARGMAX && kStreamMaxTiles * GROUPS * PW <= 64;
+  if (kOneWave && wave != 0) return;
   unsigned long long best[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) best[m] = 0ull;
   const int entries = count * GROUPS * PW;  // count is the same in every wave of the workgroup
-  for (int e = tid; e < entries; e += T) {
+  for (int e = kOneWave ? lane : tid; e < entries; e += kOneWave ? 64 : T) {
     const int p = e % PW;
     const int g = (e / PW) % GROUPS;
     const int i = e / (PW * GROUPS);
@@ -283,9 +287,15 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     }
   }
 
-  if constexpr (EPI == EPI_ARGMAX) {
-    // This workgroup's best key per input row; the finalize pass (or the gathering
-    // workgroup) reduces the workgroups.
+  if constexpr (kOneWave) {
+    // This workgroup's best key per input row (lane m publishes row m); the
+    // finalize pass (or the gathering workgroup) reduces the workgroups.
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      best[m] = wave_max_key(best[m]);
+      if (lane == m && m < M) publish_key(a, (size_t)blockIdx.x * M + m, best[m]);
+    }
+  } else if constexpr (EPI == EPI_ARGMAX) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       best[m] = wave_max_key(best[m]);
