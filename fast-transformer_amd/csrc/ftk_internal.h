@@ -155,7 +155,9 @@ __device__ void argmax_gather(const ProjArgs& a, int walkers, int tiles, unsigne
     while (need) {
       unsigned long long k[MR];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) k[m] = m < M ? take_key(a.keys + (size_t)tid * M + m) : 0ull;  // M: uniform
+      // Every load is issued (rows past M re-read row M - 1, never used): a load under
+      // a condition compiles to a branch whose join waits for it, one round trip each.
+      for (int m = 0; m < MR; ++m) k[m] = take_key(a.keys + (size_t)tid * M + (m < M ? m : M - 1));
 #pragma unroll
       for (int m = 0; m < MR; ++m)
         if (((need >> m) & 1u) && k[m] != 0ull) {
