@@ -107,3 +107,32 @@ def test_graph_of_gathered_and_two_launch_calls_replays_to_the_eager_ids(cuda, h
             assert torch.equal(out[m], eager[m]), (r, m)
         A.lm_head_argmax(other, w, g, 1e-6, logits=False)  # a two-launch call between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m", [2, 5, 8])
+def test_stream_multi_row_gather_equals_two_launch_form(cuda, m):
+    """Several x rows on the STREAM kind with at most one key word per gathering lane (4096 rows
+    walked by 256 workgroups): one launch whose gatherer reads every walker's M words at once, the
+    same logits and ids as the two-launch form of the same kernel (1024 workgroups, more than one
+    word per lane), and the key region zero afterwards."""
+    v, k = 4096, 4096
+    cfg = _native.Config(_native.KIND_STREAM, 2, 0, 1, 4)
+    p = L.plan(m, v, k, _native.EPI_ARGMAX, config=cfg, prologue=True)
+    assert p.kind == _native.KIND_STREAM and p.grid <= p.threads
+    x = seeded((m, k), seed=350 + m, device=cuda)
+    w = seeded((v, k), seed=351, scale=0.02, device=cuda)
+    g = seeded((k,), seed=352, scale=0.1, shift=1.0, device=cuda)
+    w[1234] = w[77]  # an exact tie: the lower index wins
+    top = torch.empty(m, dtype=torch.float32, device=cuda)
+    ids, logits = A.lm_head_argmax(x, w, g, 1e-6, logits=True, top=top, config=cfg)
+    torch.cuda.synchronize()
+    assert _keys_zero(cuda, m, p.grid)
+    got = to_bits(logits).reshape(m, v)
+    want = path.argmax_first(got)
+    assert np.array_equal(ids.cpu().numpy(), want)
+    assert np.array_equal(top.cpu().numpy(), bf16.to_f32(got)[np.arange(m), want])
+    two = _native.Config(_native.KIND_STREAM, 2, 0, 4, 4)
+    p2 = L.plan(m, v, k, _native.EPI_ARGMAX, config=two, prologue=True)
+    assert p2.kind == _native.KIND_STREAM and p2.grid > p2.threads  # the finalize launch
+    ids_2, logits_2 = A.lm_head_argmax(x, w, g, 1e-6, logits=True, config=two)
+    assert torch.equal(logits, logits_2) and torch.equal(ids, ids_2)
