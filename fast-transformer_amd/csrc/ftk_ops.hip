@@ -400,38 +400,42 @@ __global__ __launch_bounds__(kThreads) void argmax_block_rows_kernel(const uint1
 // Stage two: one workgroup per row picks the best of ``slots`` keys and writes
 // the id (and the winning logit) (argmax.py:34-48 _first_best). The keys were
 // just written by other CUs, so every load is a long trip: each thread issues
-// its kFinalizeLoads loads together, and 1024 threads cover 8192 slots a round.
-// Every key is zeroed once read: the key region is zero between calls, which the
+// its kFinalizeLoads loads together (unconditionally, slots past the end
+// re-reading the last one: a load under a condition compiles to a branch whose
+// join waits for it). The workgroup is as small as covers the slots in one round
+// (one wave for up to 512 slots), up to 1024 threads (8192 slots a round). Every
+// key is zeroed once read: the key region is zero between calls, which the
 // one-launch argmax (argmax_gather) relies on when it shares the workspace.
-constexpr int kFinalizeThreads = 1024;
 constexpr int kFinalizeLoads = 8;
-__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(unsigned long long* __restrict__ keys,
-                                                                           int slots, int rows, void* ids,
-                                                                           int ids_bytes, float* top) {
-  __shared__ unsigned long long red[kFinalizeThreads / 64];
+template <int T>
+__global__ __launch_bounds__(T) void argmax_finalize_kernel(unsigned long long* __restrict__ keys, int slots,
+                                                            int rows, void* ids, int ids_bytes, float* top) {
+  __shared__ unsigned long long red[T / 64];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   unsigned long long best = 0ull;
-  for (int base = 0; base < slots; base += kFinalizeLoads * kFinalizeThreads) {
+  for (int base = 0; base < slots; base += kFinalizeLoads * T) {
     unsigned long long k[kFinalizeLoads];
 #pragma unroll
     for (int u = 0; u < kFinalizeLoads; ++u) {
-      const int s = base + u * kFinalizeThreads + tid;
-      k[u] = s < slots ? keys[(size_t)s * rows + row] : 0ull;
+      const int s = base + u * T + tid;
+      k[u] = keys[(size_t)(s < slots ? s : slots - 1) * rows + row];
     }
 #pragma unroll
     for (int u = 0; u < kFinalizeLoads; ++u) {
-      const int s = base + u * kFinalizeThreads + tid;
+      const int s = base + u * T + tid;
       if (s < slots) keys[(size_t)s * rows + row] = 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kFinalizeLoads; ++u) best = key_max(best, k[u]);
   }
   best = wave_max_key(best);
-  if ((tid & 63) == 0) red[tid >> 6] = best;
-  __syncthreads();
+  if constexpr (T > 64) {
+    if ((tid & 63) == 0) red[tid >> 6] = best;
+    __syncthreads();
+    for (int w = 0; w < T / 64; ++w) best = key_max(best, red[w]);
+  }
   if (tid == 0) {
-    for (int w = 0; w < kFinalizeThreads / 64; ++w) best = key_max(best, red[w]);
     const uint32_t idx = key_index(best);
     if (ids_bytes == 8)
       reinterpret_cast<int64_t*>(ids)[row] = (int64_t)idx;
@@ -552,8 +556,14 @@ hipError_t launch_argmax(const uint16_t* logits, int rows, int vocab, void* ids,
 
 hipError_t launch_argmax_finalize(unsigned long long* keys, int slots, int M, void* ids, int ids_bytes,
                                   float* top, hipStream_t stream) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(M), dim3(kFinalizeThreads), 0, stream, keys, slots, M, ids,
-                     ids_bytes, top);
+  if (slots <= 64 * kFinalizeLoads)
+    hipLaunchKernelGGL(argmax_finalize_kernel<64>, dim3(M), dim3(64), 0, stream, keys, slots, M, ids, ids_bytes, top);
+  else if (slots <= 256 * kFinalizeLoads)
+    hipLaunchKernelGGL(argmax_finalize_kernel<256>, dim3(M), dim3(256), 0, stream, keys, slots, M, ids, ids_bytes,
+                       top);
+  else
+    hipLaunchKernelGGL(argmax_finalize_kernel<1024>, dim3(M), dim3(1024), 0, stream, keys, slots, M, ids, ids_bytes,
+                       top);
   return hipGetLastError();
 }
 
