@@ -29,7 +29,9 @@
  *     others: the extra, last workgroup of a one-launch lm_head + argmax (the
  *     STREAM kind, M = 1) reads the other workgroups' key words, with a
  *     bounded wait (1 s; then the row's id is -1). The others never wait, so
- *     its wait ends in whatever order the workgroups run.
+ *     its wait ends in whatever order the workgroups run. After an id of -1
+ *     the workspace may hold that call's late key words: zero it again before
+ *     the next call.
  */
 #ifndef FTK_H
 #define FTK_H
