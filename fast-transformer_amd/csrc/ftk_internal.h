@@ -93,33 +93,22 @@ __device__ __forceinline__ void write_id(const ProjArgs& a, int m, unsigned long
   if (a.top != nullptr) a.top[m] = late ? __uint_as_float(0x7FC00000u) : from_orderable((uint32_t)(k >> 32));
 }
 
-// The gathering workgroup (T threads) of a grid whose `walkers` tile workgroups
-// walk `tiles` tiles (walker w: tiles w, w + walkers, ..., so the first tiles %
-// walkers walkers take one tile more). Every word is read in one of two layouts:
+// The gathering workgroup (T threads) of a grid of `walkers` tile workgroups,
+// dispatched after every walker. Every word is read in one of two layouts:
 // - one row: thread t reads words t, t + T, ..., eight at a time, in walker
-//   order. The gatherer is dispatched after every walker, so the early batches
-//   are ready when it starts; it consumes them while the last walkers stream and
-//   re-reads only what is still zero (after a short sleep), so the handoff leaves
-//   about one batch of reads after the last walker's store;
-// - at most T walkers (M > 1): it first waits, with one lane and short sleeps,
-//   for the last word of the last walker with the most tiles (the walkers start
-//   in order, so by then the others are nearly all done), then thread t reads
-//   word t of each of the M <= MR rows at once.
+//   order; the early batches are ready when it starts, so it consumes them
+//   while the last walkers stream;
+// - at most T walkers (M > 1): thread t reads the M <= MR words of walker t,
+//   each thread on its own, from the gatherer's start.
 // Loads are issued together and then checked; a word that is still zero is read
-// again after a short sleep. `red` is the kernel's own LDS, T / 64 * MR words
-// (the workgroup walks no tiles, so nothing else uses it).
+// again after a short sleep, so the handoff leaves about one round of reads
+// after the last walker's store. `red` is the kernel's own LDS, T / 64 * MR
+// words (the workgroup walks no tiles, so nothing else uses it).
 template <int T, int MR>
-__device__ void argmax_gather(const ProjArgs& a, int walkers, int tiles, unsigned long long* red) {
+__device__ void argmax_gather(const ProjArgs& a, int walkers, unsigned long long* red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = a.M;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  if (M > 1 && tid == 0) {
-    const int longest = (tiles % walkers ? tiles % walkers : walkers) - 1;
-    unsigned long long* last = a.keys + (size_t)longest * M + M - 1;
-    while (take_key(last) == 0ull && __builtin_amdgcn_s_memrealtime() - t0 <= kGatherTicks)
-      __builtin_amdgcn_s_sleep(8);
-  }
-  __syncthreads();
   bool late = false;
   unsigned long long best[MR];
 #pragma unroll

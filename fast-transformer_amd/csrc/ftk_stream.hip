@@ -50,7 +50,7 @@ __global__ __launch_bounds__(64 * W) void stream_kernel(ProjArgs a, int tiles) {
     if (a.fused) {
       walkers -= kGatherExtra;
       if ((int)blockIdx.x >= walkers) {  // the extra workgroups walk no tiles; the last gathers
-        if ((int)blockIdx.x == walkers + kGatherExtra - 1) argmax_gather<T, MR>(a, walkers, tiles, &best_lds[0][0]);
+        if ((int)blockIdx.x == walkers + kGatherExtra - 1) argmax_gather<T, MR>(a, walkers, &best_lds[0][0]);
         return;
       }
     }
