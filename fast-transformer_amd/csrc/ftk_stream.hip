@@ -1,4 +1,4 @@
-// M = 1..4 skinny BF16 projection, STREAM kind: an HBM-streaming GEMV whose
+// M = 1..8 skinny BF16 projection, STREAM kind: an HBM-streaming GEMV whose
 // x slice lives in registers, for K = 512 C KW (every model shape of the path).
 //
 // Same sums, roundings and fused extras as the GEMV kind (engine/kernels/linear.py:27-47
@@ -16,10 +16,19 @@
 //   * Rolling prefetch: as each weight chunk of tile i is consumed, the load of
 //     the same chunk of tile i + 1 is issued into the register it frees, so a
 //     wave keeps RPW x C 16-byte loads in flight through its whole life.
-//   * The first tile's loads are issued before x is read and normalised.
+//   * Every load of the prologue (x, the residual, the gain) and the first
+//     tile's weights are issued before any of them is waited for; a load under
+//     a condition would compile to a branch whose join waits for it.
 //   * No barrier inside the tile loop: each wave's per-tile totals wait in LDS,
-//     and one barrier at the end lets all 256 threads combine the KW totals and
-//     run the epilogue for every output of the workgroup.
+//     and one barrier at the end lets all threads combine the KW totals and run
+//     the epilogue for every output of the workgroup (the argmax keeps one wave
+//     when every output fits it).
+//   * One wave per row group (KW = 1): a wave holds its rows' whole sums, so it
+//     stores its outputs as soon as a tile is summed, with no LDS round and no
+//     barrier, and forms its rows' norm scale itself.
+//   * lm_head + argmax can finish in the same launch: the walkers publish their
+//     keys and one extra workgroup, dispatched last, gathers them
+//     (argmax_gather).
 #include "ftk_device.h"
 #include "ftk_internal.h"
 
