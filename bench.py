@@ -547,6 +547,7 @@ def main():
     stage(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
     if not args.no_shapes:
         per_shape = shapes_table(model, step, dev, layer_graph)
+        per_shape.update(shard_table(cfg, dev))
         per_shape.update(attention_table(cfg, dev))
         if args.extras:
             per_shape.update(full_layer_table(model, dev))
@@ -906,6 +907,52 @@ def decode_model_table(cfg, dev, context=FULL_LAYER_CONTEXT):
     stage("whole decode step done")
     return {f"Qwen3-8B greedy decode step B=1 (transformers model through decode.py, attention over {context} "
             f"slots)": {**shape_entry(us, byts), "tokens_per_s": round(1e6 / us, 1)}}
+
+
+#: One GPU's share of a Qwen3-8B layer under eight-way tensor parallelism: QKV by heads, O by its
+#: input, gate/up by the intermediate rows, down by its input (the collectives are not part of this
+#: build; each projection runs at its shard's real shape).
+TP = 8
+
+
+def shard_table(cfg, dev):
+    """µs per layer of the TP = 8 shard projections (36 layers of distinct weights, one graph), at
+    M = 1, 5 and 16, with the M = 1 pure-read floor of the same launches."""
+    h, i = cfg["hidden"], cfg["inter"]
+    qkv_n = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * cfg["head_dim"] // TP
+    q_in, i_s = cfg["q_heads"] * cfg["head_dim"] // TP, i // TP
+    g = torch.Generator(device=dev).manual_seed(13)
+
+    def mk(n, k):
+        return (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    layers = [{"qkv": mk(qkv_n, h), "o": mk(h, q_in), "gate_up": mk(2 * i_s, h), "down": mk(h, i_s)}
+              for _ in range(cfg["layers"])]
+    gain = (1 + 0.1 * torch.randn((h,), generator=g, device=dev)).to(torch.bfloat16)
+    out = {}
+    for m in (1, 5, 16):
+        x = torch.randn((m, h), generator=g, device=dev).to(torch.bfloat16)
+        attn = torch.randn((m, q_in), generator=g, device=dev).to(torch.bfloat16)
+        act = torch.randn((m, i_s), generator=g, device=dev).to(torch.bfloat16)
+
+        def layer_set(x=x, attn=attn, act=act):
+            for lw in layers:
+                L.rms_norm_linear(x, gain, EPS, lw["qkv"])
+                L.linear(attn, lw["o"])
+                S.gate_up_swiglu(x, lw["gate_up"], gain, EPS)
+                L.linear(act, lw["down"])
+        graph = capture(layer_set)  # a new shape's first eager call selects its launch; no knob re-judging here
+        us = time_graph(graph, reps=5) / cfg["layers"]
+        del graph
+        byts = ((2 * qkv_n * h + 2 * m * h + 2 * m * qkv_n + 2 * h) + (2 * h * q_in + 2 * m * q_in + 2 * m * h) +
+                (2 * 2 * i_s * h + 2 * m * h + 2 * m * i_s + 2 * h) + (2 * h * i_s + 2 * m * i_s + 2 * m * h))
+        entry = shape_entry(us, byts)
+        if m == 1:
+            floor_us = sum(read_floor([lw[key] for lw in layers], reps=3)[0] for key in ("qkv", "o", "gate_up", "down"))
+            entry = {**entry, "read_floor_us": round(floor_us, 3), "over_floor_us": round(us - floor_us, 3)}
+        out[f"TP{TP} shard 8B layer M={m} (QKV {qkv_n}x{h}, O {h}x{q_in}, gate/up 2x{i_s}x{h}, down {h}x{i_s})"] = entry
+        stage(f"TP{TP} shard M={m} done")
+    del layers
+    return out
 
 
 def attention_table(cfg, dev):

@@ -266,7 +266,14 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     // the shape.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     const bool stage = M >= 5 && stage_default(M, epi, pro, N, K).t != 0;
-    const bool ring = ring_ok && ring_preferred(M, epi) && ring_default(M, epi, pro, N, K, cus).kw != 0;
+    const RingDefault rd = ring_ok && ring_preferred(M, epi) ? ring_default(M, epi, pro, N, K, cus)
+                                                              : RingDefault{0, 0, 0, 0};
+    // RING holds one workgroup per CU: where its tiles would leave more than half
+    // the CUs idle and QUAD is preferred at these rows, QUAD's smaller tiles keep
+    // more of them streaming (a Qwen3-8B eight-way tensor-parallel shard's QKV,
+    // 768 x 4096 with the norm, at M = 5: 64 RING tiles 7.80 us, QUAD 6.55).
+    const bool ring = rd.kw != 0 && (ring_tiles(epi, (int)N, rd.rows) >= cus / 2 || !quad ||
+                                     !quad_preferred(M, epi, pro));
     if (K % 8)
       kind = FTK_KIND_GENERIC;
     else if (ring)
@@ -353,7 +360,12 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     if (M > kQuadMaxRows) return FTK_ERR_UNSUPPORTED;
     const QuadDefault d = quad_default(M, epi, pro, N, K);
     const int kw = cfg && cfg->waves ? cfg->waves : d.kw;
-    const int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : d.rows;
+    int rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : d.rows;
+    // Four rows per tile where the default would leave more than half the CUs
+    // without a tile (the shard's QKV at M = 5: 4-row tiles 6.55 us, 8-row 7.08).
+    if (!(cfg && cfg->rows_per_wave) && gemv_tiles(epi, (int)N, rows, kw) < cus / 2 &&
+        quad_supported((int)M, 4, (int)K, kw, epi, pro))
+      rows = 4;
     const int c = quad_segments((int)K, kw);
     if (c == 0) return FTK_ERR_UNSUPPORTED;  // K is not 128 C KW
     if (!quad_supported((int)M, rows, (int)K, kw, epi, pro)) return FTK_ERR_INVALID;

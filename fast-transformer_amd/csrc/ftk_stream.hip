@@ -348,15 +348,20 @@ typedef void (*StreamKernel)(ProjArgs, int);
   FTK_STREAM_SHAPE(8, 4, 3, 8, PRO, EPI)
 
 // One wave per row group (KW = 1, whole rows per wave, no barrier in the
-// epilogue) at one x row: the K of the Qwen3 shapes up to 4096. One row per wave
-// only where there is no SwiGLU (which pairs a gate and an up row).
+// epilogue) at one x row: the K of the Qwen3 shapes up to 4096, and 512 / 1536
+// (the O and down rows of a Qwen3-8B eight-way tensor-parallel shard). One row
+// per wave only where there is no SwiGLU (which pairs a gate and an up row).
 #define FTK_STREAM_SHAPES_KW1(PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 1, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 2, 2, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 2, 3, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 2, 4, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 2, 6, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 2, 8, 1, PRO, EPI)
 #define FTK_STREAM_SHAPES_KW1_ROW(PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 1, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 1, 2, 1, PRO, EPI) \
+  FTK_STREAM_SHAPE(1, 1, 3, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 1, 4, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 1, 6, 1, PRO, EPI) \
   FTK_STREAM_SHAPE(1, 1, 8, 1, PRO, EPI)

@@ -162,7 +162,7 @@ def test_default_plan_is_stream_for_model_shapes(cuda):
 
 #: One wave per row group (KW = 1) at one x row: whole rows per wave, no LDS round or barrier in the
 #: STORE / SwiGLU epilogue (rows per wave, chunks per lane C; K = 512 C).
-STREAM_SHAPES_KW1 = ((1, 2), (2, 2), (1, 4), (2, 4), (1, 6), (2, 6), (1, 8), (2, 8))
+STREAM_SHAPES_KW1 = ((1, 1), (2, 1), (1, 2), (2, 2), (1, 3), (2, 3), (1, 4), (2, 4), (1, 6), (2, 6), (1, 8), (2, 8))
 
 
 @pytest.mark.parametrize("rpw,c", STREAM_SHAPES_KW1)
