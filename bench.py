@@ -105,12 +105,15 @@ class Step:
         self.attn = torch.randn((m, model.q), generator=g, device=device).to(torch.bfloat16)
         self.resid = torch.randn((m, cfg["hidden"]), generator=g, device=device).to(torch.bfloat16)
         self.top = torch.empty(m, dtype=torch.float32, device=device)
+        # the norms' sums of squares, handed from each producer to the norm that reads its rows
+        # (RING launches, 5..16 rows; elsewhere each norm reads its rows)
+        self.sums = L.SumSq()
 
     def layer(self, lw, h):
-        qkv = L.rms_norm_linear(h, lw["ln1"], EPS, lw["qkv"])
-        o = L.linear(self.attn, lw["o"])
-        act = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS)
-        return qkv, L.linear(act, lw["down"])
+        qkv = L.rms_norm_linear(h, lw["ln1"], EPS, lw["qkv"], sumsq=self.sums)
+        o = L.linear_sumsq(self.attn, lw["o"], self.sums)
+        act = S.gate_up_swiglu(o, lw["gate_up"], lw["ln2"], EPS, sumsq=self.sums)
+        return qkv, L.linear_sumsq(act, lw["down"], self.sums)
 
     def layers(self):
         h = self.h
@@ -134,16 +137,16 @@ class Step:
         each norm then reads the stored stream as a plain x."""
         resid = self.resid
         for lw in self.model.layers:
-            L.rms_norm_linear(resid, lw["ln1"], EPS, lw["qkv"])
-            resid = L.linear_residual(self.attn, lw["o"], resid)
-            act = S.gate_up_swiglu(resid, lw["gate_up"], lw["ln2"], EPS)
-            resid = L.linear_residual(act, lw["down"], resid)
+            L.rms_norm_linear(resid, lw["ln1"], EPS, lw["qkv"], sumsq=self.sums)
+            resid = L.linear_residual(self.attn, lw["o"], resid, sumsq=self.sums)
+            act = S.gate_up_swiglu(resid, lw["gate_up"], lw["ln2"], EPS, sumsq=self.sums)
+            resid = L.linear_residual(act, lw["down"], resid, sumsq=self.sums)
         return resid
 
     def run(self):
         h = self.layers()
         return A.lm_head_argmax(h, self.model.head, self.model.final_norm, EPS, logits=True, top=self.top,
-                                ids_dtype=torch.int32)
+                                ids_dtype=torch.int32, sumsq=self.sums)
 
 
 def capture(fn, warm=2):

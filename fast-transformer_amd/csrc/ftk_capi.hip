@@ -740,9 +740,21 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
     if (ids == nullptr || (ids_bytes != 4 && ids_bytes != 8)) return FTK_ERR_INVALID;
     if (workspace == nullptr) return FTK_ERR_WORKSPACE;
   }
-  ftk_rows r = {nullptr, nullptr, nullptr, 0, 0};
+  ftk_rows r = {nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr};
   if (rows != nullptr) r = *rows;
   const bool extra = r.residual != nullptr || r.sum != nullptr || r.x_ids != nullptr;
+  if (r.sumsq != nullptr) {  // the norm's sums of x's rows, in place of the rows
+    if (gamma == nullptr || extra) return FTK_ERR_INVALID;
+    if (K % 16 || !aligned16(r.sumsq)) return FTK_ERR_UNSUPPORTED;
+  }
+  if (r.sumsq_out != nullptr) {
+    if (epilogue != FTK_EPI_STORE) return FTK_ERR_UNSUPPORTED;
+    if ((reinterpret_cast<uintptr_t>(r.sumsq_out) & 3) != 0) return FTK_ERR_INVALID;
+    const int64_t sq_bytes = M * ((N + 15) / 16) * 4;
+    if (overlaps(r.sumsq_out, sq_bytes, y, M * N * 2) || overlaps(r.sumsq_out, sq_bytes, x, M * K * 2) ||
+        overlaps(r.sumsq_out, sq_bytes, out_add, M * N * 2) || overlaps(r.sumsq_out, sq_bytes, r.sumsq, M * (K / 16) * 4))
+      return FTK_ERR_INVALID;
+  }
   if (extra) {
     if (gamma == nullptr) return FTK_ERR_INVALID;  // the rows feed the norm
     if (r.x_ids != nullptr && ((r.x_ids_bytes != 4 && r.x_ids_bytes != 8) || r.x_rows < 1)) return FTK_ERR_INVALID;
@@ -796,6 +808,11 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
     return FTK_ERR_UNSUPPORTED;
   // The RING kind loads x rows as they are: no residual add in its prologue.
   if (p.kind == FTK_KIND_RING && r.residual != nullptr) return FTK_ERR_UNSUPPORTED;
+  // Row sums of squares travel between RING launches only (16-row STORE tiles write them).
+  if (r.sumsq != nullptr && p.kind != FTK_KIND_RING) return FTK_ERR_UNSUPPORTED;
+  if (r.sumsq_out != nullptr && (p.kind != FTK_KIND_RING || p.rows_per_wave != 16)) return FTK_ERR_UNSUPPORTED;
+  a.sumsq = r.sumsq;
+  a.sumsq_out = r.sumsq_out;
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   // Greedy argmax in one launch (argmax_gather) for the STREAM kind: one row, or at most one key
@@ -848,22 +865,30 @@ int ftk_project_bf16(const void* x, const void* gamma, float eps, const void* w,
                       workspace_bytes, cfg, nullptr, stream);
 }
 
-int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
-                         int64_t K, const ftk_config* cfg, void* stream) {
+int ftk_project_add_rows_bf16(const void* x, const ftk_rows* rows, const void* w, const void* residual, void* y,
+                              int64_t M, int64_t N, int64_t K, const ftk_config* cfg, void* stream) {
   if (residual == nullptr || y == nullptr) return FTK_ERR_INVALID;
+  // Only the sums of the stored outputs: the prologue's fields describe a norm, which this call has not.
+  if (rows != nullptr && (rows->residual || rows->sum || rows->x_ids || rows->sumsq)) return FTK_ERR_INVALID;
   // y may be the residual itself (each output reads its own residual element,
   // then writes it), but no other overlap with the inputs.
   const int64_t out_bytes = M * N * 2;
   if (y != residual && overlaps(y, out_bytes, residual, out_bytes)) return FTK_ERR_INVALID;
   if (overlaps(y, out_bytes, x, M * K * 2) || overlaps(y, out_bytes, w, N * K * 2)) return FTK_ERR_INVALID;
-  int st = project_impl(x, nullptr, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, cfg,
+  int st = project_impl(x, rows, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, cfg,
                         residual, stream);
-  if (st == FTK_ERR_UNSUPPORTED && cfg == nullptr) {  // an unaligned pointer or an unsplit MFMA x slice
+  // An unaligned pointer or an unsplit MFMA x slice: the generic kind, which writes no sums.
+  if (st == FTK_ERR_UNSUPPORTED && cfg == nullptr && (rows == nullptr || rows->sumsq_out == nullptr)) {
     const ftk_config c = {FTK_KIND_GENERIC, 0, 0, 0, 0};
     st = project_impl(x, nullptr, nullptr, 0.f, w, y, M, N, K, FTK_EPI_STORE, nullptr, 0, nullptr, nullptr, 0, &c,
                       residual, stream);
   }
   return st;
+}
+
+int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
+                         int64_t K, const ftk_config* cfg, void* stream) {
+  return ftk_project_add_rows_bf16(x, nullptr, w, residual, y, M, N, K, cfg, stream);
 }
 
 int ftk_linear_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {

@@ -40,6 +40,13 @@ struct ProjArgs {
   // stored value is then bf16(bf16(y) + out_add[m, n]) (the add of add_rms_norm
   // moved into the producer; it may alias y).
   const uint16_t* out_add;   // [M, N] or null
+  // The norm's statistics handed from one projection to the next (RING kind only):
+  // sumsq_out (STORE, 16-row tiles) receives, for each output row m and 16-column
+  // part t, the FP32 sum of the squares of the stored BF16 outputs, at
+  // [m][ceil(N / 16)] + t; a prologue given sumsq ([M][K / 16], written that way for
+  // its x) sums those parts instead of reading the rows of x.
+  const float* sumsq;
+  float* sumsq_out;
 };
 
 // The BF16 bits a STORE epilogue writes for output (m, n) with FP32 sum s.

@@ -218,6 +218,9 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   constexpr int GPT = PRO ? (GCH + 64 * KW - 1) / (64 * KW) : 1;
   constexpr int RPW = (16 + KW - 1) / KW;  // rows per wave at most
   constexpr int CPL = C * KW / 4;          // chunks per lane per row: K / 512
+  constexpr int SPL = (CPL + 7) / 8;       // 4-part chunks per lane per row of sumsq: K / 16 / 256
+  const int parts = K / 16;                // parts per row of sumsq
+  const bool from_sums = PRO && a.sumsq != nullptr;  // uniform
   u32x4_t gl[GPT];
   u32x4_t xv[PRO ? RPW : 1][PRO ? CPL : 1];
   if constexpr (PRO) {
@@ -227,12 +230,21 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       const int c = tid + i * 64 * KW;
       gl[i] = asm_load16(a.gamma + (size_t)(c < GCH ? c : 0) * 8);
     }
-    // Rows kw + i KW; waves past the last row load nothing (the wait below counts
-    // only the units issued after these loads).
+    // Rows kw + i KW (their parts of sumsq, or the rows themselves); waves past the
+    // last row load nothing (the wait below counts only the units issued after
+    // these loads). Lanes past the last part read the row's last four (discarded).
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int m = kw + i * KW;
-      if (m < M) {  // wave-uniform
+      if (m < M && from_sums) {  // wave-uniform
+#pragma unroll
+        for (int c = 0; c < SPL; ++c) {
+          const int at = (lane + 64 * c) * 4;
+          xv[i][c] = asm_load16(a.sumsq + (size_t)m * parts + (at < parts ? at : parts - 4));
+        }
+#pragma unroll
+        for (int c = SPL; c < CPL; ++c) xv[i][c] = u32x4_t{0u, 0u, 0u, 0u};
+      } else if (m < M) {  // wave-uniform
         const uint16_t* xr = x_row(a, m);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) xv[i][c] = asm_load16(xr + (size_t)(lane + 64 * c) * 8);
@@ -277,8 +289,16 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       float ss = 0.f;
+      if (from_sums) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) ss = sum_squares8(xv[i][c], ss);
+        for (int c = 0; c < SPL; ++c) {
+          const f32x4_t v = __builtin_bit_cast(f32x4_t, xv[i][c]);
+          if ((lane + 64 * c) * 4 < parts) ss += (v[0] + v[1]) + (v[2] + v[3]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) ss = sum_squares8(xv[i][c], ss);
+      }
       const float total = wave_sum(ss);
       const int m = kw + i * KW;
       if (lane == 0 && m < 16) lds_write_f32(red + m, total);
@@ -346,6 +366,34 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (n0 + r < a.N) best = key_max(best, argmax_key(bf16_to_f32(bits[r]), (uint32_t)(n0 + r)));
+        }
+      }
+      // The stored rows' sums of squares by tile (16 outputs), when asked: the same
+      // values again (the parked sums and the residual), squared and summed over the
+      // wave's lanes ln, ln + 16, ln + 32, ln + 48 (every lane of a wave takes the
+      // same entries of this loop: 64 per tile).
+      if constexpr (EPI == EPI_STORE && RT == 16) {
+        if (a.sumsq_out != nullptr) {
+          for (int e = tid; e < entries; e += 64 * KW) {
+            const int ln = e & 63, i = e >> 6;
+            const int ll = ln & 15, gg = ln >> 4;
+            const int tl = tile_at(done + i);
+            float sq = 0.f;
+            if (ll < M) {
+              f32x4_t s = part[i][0][0][ln];
+#pragma unroll
+              for (int w = 1; w < KW; ++w) s += part[i][w][0][ln];
+              const int n0 = tl * 16 + 4 * gg;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float v = n0 + r < a.N ? bf16_to_f32(store_bits(a, s[r], ll, n0 + r)) : 0.f;
+                sq += v * v;
+              }
+            }
+            sq += __shfl_xor(sq, 16);
+            sq += __shfl_xor(sq, 32);
+            if (gg == 0 && ll < M) a.sumsq_out[(size_t)ll * ((a.N + 15) / 16) + tl] = sq;
+          }
         }
       }
     }

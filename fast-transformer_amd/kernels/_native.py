@@ -48,10 +48,11 @@ class Plan(ctypes.Structure):
 
 
 class Rows(ctypes.Structure):
-    """ftk_rows: the prologue's residual, stored sum and gathered row indices (NULL = absent)."""
+    """ftk_rows: the prologue's residual, stored sum and gathered row indices, and the norm's sums of
+    squares handed between RING launches (sumsq in, sumsq_out written) (NULL = absent)."""
 
     _fields_ = [("residual", _c_void_p), ("sum", _c_void_p), ("x_ids", _c_void_p), ("x_ids_bytes", _int),
-                ("x_rows", _i64)]
+                ("x_rows", _i64), ("sumsq", _c_void_p), ("sumsq_out", _c_void_p)]
 
 
 class AttnConfig(ctypes.Structure):
@@ -92,6 +93,8 @@ SIGNATURES = {
                                 _c_void_p, _int, _c_void_p, _c_void_p, _i64, ctypes.POINTER(Config), _c_void_p]),
     "ftk_project_add_bf16": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                     ctypes.POINTER(Config), _c_void_p]),
+    "ftk_project_add_rows_bf16": (_int, [_c_void_p, ctypes.POINTER(Rows), _c_void_p, _c_void_p, _c_void_p, _i64,
+                                         _i64, _i64, ctypes.POINTER(Config), _c_void_p]),
     "ftk_project_rows_bf16": (_int, [_c_void_p, ctypes.POINTER(Rows), _c_void_p, _float, _c_void_p, _c_void_p,
                                      _i64, _i64, _i64, _int, _c_void_p, _int, _c_void_p, _c_void_p, _i64,
                                      ctypes.POINTER(Config), _c_void_p]),

@@ -42,13 +42,14 @@ def argmax(logits, block=8192, top=None):
 
 
 def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None, ids_dtype=torch.int64,
-                   config=None, residual=None):
+                   config=None, residual=None, sumsq=None):
     """(ids, logits or None): greedy ids of rms_norm?(x [+ residual]) @ weight.T in one projection kernel.
 
     Ties go to the lowest index of the BF16-rounded logits. ``residual`` makes
     the prologue the final add_rms_norm of engine/decode.py:264-265 (its sum is
     not needed afterwards). Shapes the fused kernel does not take run the norm,
-    projection and argmax kernels in turn.
+    projection and argmax kernels in turn. ``sumsq``: a ``kernels.linear.SumSq`` that may
+    hold x's sums of squares for the norm.
     """
     _native.require_gpu(x, weight, norm_weight, top, residual)
     if residual is not None and norm_weight is None:
@@ -75,7 +76,8 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
         def run(choice, w, inp=flat):
             lg = torch.empty((inp.shape[0], w.shape[0]), device=inp.device, dtype=torch.bfloat16)
             tok = torch.empty((inp.shape[0],), device=inp.device, dtype=ids_dtype)
-            st = fused_project(inp, w, _native.EPI_ARGMAX, lg, norm_weight, eps, ids=tok, config=_as_config(choice))
+            st = fused_project(inp, w, _native.EPI_ARGMAX, lg, norm_weight, eps, ids=tok, config=_as_config(choice),
+                               sumsq=sumsq)
             return lg if st == _native.FTK_OK else None
 
         def native_logits(w, inp=flat):
@@ -91,11 +93,11 @@ def lm_head_argmax(x, weight, norm_weight=None, eps=1e-6, logits=True, top=None,
             full = native_logits(weight)
             return argmax(full, top=top).to(ids_dtype), (full.reshape(*shape[:-1], v) if logits else None)
         status = fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, ids=ids, top=top,
-                               config=_as_config(choice))
+                               config=_as_config(choice), sumsq=sumsq)
     else:
         status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
             fused_project(flat, weight, _native.EPI_ARGMAX, out, norm_weight, eps, residual=res, ids=ids, top=top,
-                          config=config)
+                          config=config, sumsq=sumsq)
     if status != _native.FTK_OK:
         if residual is not None:
             xn = add_rms_norm(x, residual, norm_weight, eps)[0]

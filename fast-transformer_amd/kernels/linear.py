@@ -73,42 +73,104 @@ def _as_rows(x):
     return x.reshape(rows, x.shape[-1]).contiguous()
 
 
+class SumSq:
+    """The RMSNorm statistics of a row stream, handed from the projection that writes the rows to the
+    norm that reads them next (``ftk_rows.sumsq_out`` / ``sumsq``; the RING kind, 2..16 rows).
+
+    A projection given this object without a norm (``linear_sumsq``, ``project``, ``linear_residual``)
+    writes, beside its output ``y`` [M, N], the FP32 sums of the squares of each row's stored BF16
+    values by 16-column part. A later norm-prologue call over that same ``y`` (``rms_norm_linear``,
+    ``gate_up_swiglu``, ``lm_head_argmax`` given the object) sums those parts instead of reading the
+    rows: its kernel need not wait for every row of x before its first products. The sums are used
+    only while they describe the call's x: the same tensor (address and shape; the object keeps its
+    storage alive), unchanged since it was written (version counter). Otherwise, or where either
+    launch is not RING, the norm reads x as usual. One object serves a whole decode step: each producer overwrites the
+    sums, and each norm reads the sums of its own input.
+    """
+
+    def __init__(self):
+        self._buf = None
+        self._src = None
+
+    def _out(self, y):
+        """Buffer for the sums of ``y`` [M, N]; the previous sums stop counting."""
+        self._src = None
+        need = y.shape[0] * ((y.shape[1] + 15) // 16)
+        buf = self._buf
+        if buf is None or buf.device != y.device or buf.numel() < need:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("SumSq buffers must be sized during eager warmup, before graph capture")
+            if buf is not None:
+                _native._RETIRED.append(buf)  # a captured graph may hold its address
+            buf = self._buf = torch.empty(max(need, 4096), dtype=torch.float32, device=y.device)
+        return buf
+
+    def _wrote(self, y):
+        # Holding y's storage keeps its address from being handed to another tensor meanwhile.
+        self._src = (y.untyped_storage(), y.data_ptr(), tuple(y.shape), y._version, y.device)
+
+    def _of(self, x):
+        """The sums of ``x`` [M, K], or None where they do not describe it."""
+        src = self._src
+        if src is None or (x.data_ptr(), tuple(x.shape), x._version, x.device) != src[1:]:
+            return None
+        return self._buf
+
+
 def fused_project(x, weight, epilogue, out, norm_weight=None, eps=1e-6, residual=None, x_ids=None, summed=None,
-                  ids=None, top=None, config=None):
+                  ids=None, top=None, config=None, sumsq=None):
     """One projection launch with its fused prologue / epilogue (ftk_project_rows_bf16).
 
     ``x`` is [M, K] (or, with ``x_ids``, the [rows, K] table they index);
     ``residual`` [M, K] is added before the norm and ``summed`` [M, K] receives
-    the rows the norm read. Returns the C status: FTK_OK, or
+    the rows the norm read. ``sumsq`` (a ``SumSq``): with the norm, its sums of x
+    replace the norm's read of x where they describe x; without it (the STORE
+    epilogue), the call writes the sums of ``out``. Returns the C status: FTK_OK, or
     FTK_ERR_UNSUPPORTED when the shape / alignment has no fused kernel (the
     caller then composes the separate kernels). Raises on anything else.
     """
     m = x_ids.numel() if x_ids is not None else x.shape[0]
     k = x.shape[1]
     n = weight.shape[0]
-    rows = None
-    if residual is not None or summed is not None or x_ids is not None:
-        ids_bytes = 0 if x_ids is None else {torch.int64: 8, torch.int32: 4}[x_ids.dtype]
-        table_rows = x.shape[0] if x_ids is not None else 0
-        rows = ctypes.byref(_native.Rows(_native.ptr(residual), _native.ptr(summed), _native.ptr(x_ids), ids_bytes,
-                                         table_rows))
+    sq_in = sq_out = None
+    if sumsq is not None:
+        if norm_weight is not None:
+            if residual is None and summed is None and x_ids is None:
+                sq_in = sumsq._of(x)
+        elif epilogue == _native.EPI_STORE:
+            sq_out = sumsq._out(out)
     ws = _native.project_workspace(x.device, m, n, k, epilogue, config, prologue=norm_weight is not None,
                                    residual=residual is not None)
     ids_bytes = 0 if ids is None else {torch.int64: 8, torch.int32: 4}[ids.dtype]
-    status = _native.try_call(
-        "ftk_project_rows_bf16", _native.ptr(x), rows, _native.ptr(norm_weight), float(eps), _native.ptr(weight),
-        _native.ptr(out), m, n, k, epilogue, _native.ptr(ids), ids_bytes, _native.ptr(top), _native.ptr(ws),
-        ws.numel(), config, _native.stream_of(x))
+
+    def call(sq_in, sq_out):
+        rows = None
+        if residual is not None or summed is not None or x_ids is not None or sq_in is not None or sq_out is not None:
+            x_ids_bytes = 0 if x_ids is None else {torch.int64: 8, torch.int32: 4}[x_ids.dtype]
+            table_rows = x.shape[0] if x_ids is not None else 0
+            rows = ctypes.byref(_native.Rows(_native.ptr(residual), _native.ptr(summed), _native.ptr(x_ids),
+                                             x_ids_bytes, table_rows, _native.ptr(sq_in), _native.ptr(sq_out)))
+        return _native.try_call(
+            "ftk_project_rows_bf16", _native.ptr(x), rows, _native.ptr(norm_weight), float(eps),
+            _native.ptr(weight), _native.ptr(out), m, n, k, epilogue, _native.ptr(ids), ids_bytes,
+            _native.ptr(top), _native.ptr(ws), ws.numel(), config, _native.stream_of(x))
+
+    status = call(sq_in, sq_out)
+    if status == _native.FTK_ERR_UNSUPPORTED and (sq_in is not None or sq_out is not None):
+        status = call(None, None)  # not a RING launch: the norm reads x, no sums are written
+    elif status == _native.FTK_OK and sq_out is not None:
+        sumsq._wrote(out)
     if status not in (_native.FTK_OK, _native.FTK_ERR_UNSUPPORTED):
         raise _native.FtkError("ftk_project_rows_bf16", status)
     return status
 
 
-def project(x, weight, config=None, out=None):
+def project(x, weight, config=None, out=None, sumsq=None):
     """y[M, N] = x[M, K] @ weight[N, K].T on the GPU (the device work of _project, linear.py:178-314).
 
-    ``config`` is a ``_native.Config`` (None = planner default). Raises on any
-    unsupported input; there is no fallback here.
+    ``config`` is a ``_native.Config`` (None = planner default). ``sumsq`` (a ``SumSq``) receives
+    the rows' sums of squares for the norm that reads y next. Raises on any unsupported input;
+    there is no fallback here.
     """
     _native.require_gpu(x, weight)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
@@ -123,7 +185,7 @@ def project(x, weight, config=None, out=None):
         out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
     if m == 0:
         return out
-    status = fused_project(x, weight, _native.EPI_STORE, out, config=config)
+    status = fused_project(x, weight, _native.EPI_STORE, out, config=config, sumsq=sumsq)
     if status == _native.FTK_ERR_UNSUPPORTED:
         if config is not None:
             raise _native.FtkError("ftk_project_rows_bf16", status)
@@ -133,12 +195,13 @@ def project(x, weight, config=None, out=None):
     return out
 
 
-def rms_norm_linear(x, norm_weight, eps, weight, config=None):
+def rms_norm_linear(x, norm_weight, eps, weight, config=None, sumsq=None):
     """rms_norm(x, norm_weight, eps) @ weight.T with the norm folded into the projection's prologue.
 
     Cast order of engine/kernels/rmsnorm.py:35-46 (normalised value rounded to
     BF16 before the gain multiply). Shapes no fused kernel takes (K % 8 != 0,
-    unaligned) run the separate norm kernel, then ``linear``.
+    unaligned) run the separate norm kernel, then ``linear``. ``sumsq``: a ``SumSq``
+    that may hold x's sums of squares (written by the projection that produced x).
     """
     _native.require_gpu(x, norm_weight, weight)
     from kernels.rmsnorm import rms_norm
@@ -152,7 +215,7 @@ def rms_norm_linear(x, norm_weight, eps, weight, config=None):
 
     def fused(cfg, w, inp=flat):
         y = torch.empty((inp.shape[0], w.shape[0]), device=inp.device, dtype=torch.bfloat16)
-        status = fused_project(inp, w, _native.EPI_STORE, y, norm_weight, eps, config=cfg)
+        status = fused_project(inp, w, _native.EPI_STORE, y, norm_weight, eps, config=cfg, sumsq=sumsq)
         return y if status == _native.FTK_OK else None
 
     if config is None and _fusable(flat, weight, norm_weight):
@@ -482,14 +545,15 @@ def refine(step_seconds, rows, seconds=10.0):
     return best
 
 
-def linear_residual(x, weight, residual, config=None):
+def linear_residual(x, weight, residual, config=None, sumsq=None):
     """bf16(linear(x, weight) + residual): a projection whose output joins the residual stream.
 
     The add of add_rms_norm (engine/kernels/rmsnorm.py:86-95) runs in the projection's epilogue
     (ftk_project_add_bf16). Where engine/decode.py:236-243 / :258-261 add the O and down outputs to
     the residual, the result is add_rms_norm's ``summed`` bit for bit, so the next norm reads it as a
     plain x and no prologue reads the residual again. Neither input is modified. Every row count
-    runs this library's kernels (the MFMA kind from 17 rows).
+    runs this library's kernels (the MFMA kind from 17 rows). ``sumsq`` (a ``SumSq``) receives the
+    new stream's sums of squares for the norm that reads it next (ftk_project_add_rows_bf16).
     """
     _native.require_gpu(x, weight, residual)
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
@@ -508,6 +572,16 @@ def linear_residual(x, weight, residual, config=None):
     if m == 0:
         return out.reshape(*x.shape[:-1], n)
     cfg = ctypes.byref(config) if config is not None else None
+    if sumsq is not None:
+        rows = _native.Rows(None, None, None, 0, 0, None, _native.ptr(sumsq._out(out)))
+        status = _native.try_call("ftk_project_add_rows_bf16", _native.ptr(flat), ctypes.byref(rows),
+                                  _native.ptr(weight), _native.ptr(res), _native.ptr(out), m, n, k, cfg,
+                                  _native.stream_of(flat))
+        if status == _native.FTK_OK:
+            sumsq._wrote(out)
+            return out.reshape(*x.shape[:-1], n)
+        if status != _native.FTK_ERR_UNSUPPORTED:  # not a RING launch: no sums, the call below
+            raise _native.FtkError("ftk_project_add_rows_bf16", status)
     _native.call("ftk_project_add_bf16", _native.ptr(flat), _native.ptr(weight), _native.ptr(res), _native.ptr(out),
                  m, n, k, cfg, _native.stream_of(flat))
     return out.reshape(*x.shape[:-1], n)
@@ -520,6 +594,17 @@ def keep_native(rows, weight):
 
 def linear(x, weight, split_ok=False):
     """x @ weight.T in BF16 (linear.py:489-523). ``split_ok`` is accepted; the result is always BF16."""
+    return _linear(x, weight, None)
+
+
+def linear_sumsq(x, weight, sumsq):
+    """``linear(x, weight)`` whose output an RMSNorm reads next: the launch also writes the output
+    rows' sums of squares into ``sumsq`` (a ``SumSq``), where it is a RING launch. Not a reference
+    call: the reference's norm reads its input rows (engine/kernels/rmsnorm.py:21-46)."""
+    return _linear(x, weight, sumsq)
+
+
+def _linear(x, weight, sumsq):
     rows = x.numel() // x.shape[-1]
     if rows > MAX_ROWS or x.dtype != torch.bfloat16 or not weight.is_contiguous():
         return F.linear(x, weight)
@@ -534,7 +619,7 @@ def linear(x, weight, split_ok=False):
     choice = _choice("linear", flat, weight, run, lambda w, inp=flat: F.linear(inp, w))
     if choice == "native":
         return F.linear(x, weight)
-    out = project(flat, weight, _as_config(choice))
+    out = project(flat, weight, _as_config(choice), sumsq=sumsq)
     return out.reshape(*x.shape[:-1], weight.shape[0])
 
 

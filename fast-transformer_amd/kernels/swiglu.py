@@ -34,12 +34,13 @@ def swiglu(packed):
     return output
 
 
-def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, residual=None):
+def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, residual=None, sumsq=None):
     """swiglu(rms_norm?(x [+ residual]) @ gate_up_weight.T) in one projection kernel; [..., I] BF16.
 
     With ``residual`` the prologue is add_rms_norm (engine/kernels/rmsnorm.py:75-125,
     the post-attention norm of engine/decode.py:258-261) and the result is
-    ``(activation, x + residual)``: the sum is the next residual stream.
+    ``(activation, x + residual)``: the sum is the next residual stream. ``sumsq``: a
+    ``kernels.linear.SumSq`` that may hold x's sums of squares for the norm.
     """
     _native.require_gpu(x, gate_up_weight, norm_weight, residual)
     if residual is not None and norm_weight is None:
@@ -65,7 +66,8 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
         # selected like a plain projection, under its own key (kernels/linear.py _choice)
         def run(choice, w, inp=flat):
             y = torch.empty((inp.shape[0], w.shape[0] // 2), device=inp.device, dtype=torch.bfloat16)
-            st = fused_project(inp, w, _native.EPI_SWIGLU, y, norm_weight, eps, config=_as_config(choice))
+            st = fused_project(inp, w, _native.EPI_SWIGLU, y, norm_weight, eps, config=_as_config(choice),
+                               sumsq=sumsq)
             return y if st == _native.FTK_OK else None
 
         def native(w, inp=flat):
@@ -76,11 +78,11 @@ def gate_up_swiglu(x, gate_up_weight, norm_weight=None, eps=1e-6, config=None, r
             # the form selection timed: torch's GEMM itself, never a second selection by linear()
             return native(gate_up_weight).reshape(*shape[:-1], n // 2)
         status = fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps,
-                               config=_as_config(choice))
+                               config=_as_config(choice), sumsq=sumsq)
     else:
         status = _native.FTK_ERR_UNSUPPORTED if prefer_native(m, config) else \
             fused_project(flat, gate_up_weight, _native.EPI_SWIGLU, out, norm_weight, eps, residual=res,
-                          summed=summed, config=config)
+                          summed=summed, config=config, sumsq=sumsq)
     if status != _native.FTK_OK:
         from kernels.rmsnorm import add_rms_norm, rms_norm
         if residual is not None:

@@ -25,6 +25,8 @@
  *     leaves the ones it used zero again (the one-launch argmax reads a
  *     non-zero word as a key of the current call). Nothing else carries over
  *     between calls. Calls that share a workspace must not run concurrently.
+ *     (The norm's row sums of ftk_rows.sumsq_out / sumsq are the caller's own
+ *     buffer, written by one call for a later one to read.)
  *   - No kernel uses device-scope fences or tickets. One workgroup waits on
  *     others: the extra, last workgroup of a one-launch lm_head + argmax (the
  *     STREAM kind, M = 1) reads the other workgroups' key words, with a
@@ -217,6 +219,19 @@ typedef struct ftk_rows {
   int64_t x_rows;        /* rows of the table x (required, >= 1, with x_ids). The ids live on the
                             device, so the device clamps them into the table: an id below 0 reads
                             row 0 and an id at or past x_rows reads row x_rows - 1 */
+  /* The norm's statistics carried from the projection that writes a row stream to the
+   * norm that reads it (the RING kind, M = 2..16). No counterpart in the reference,
+   * whose norm reads its input rows (engine/kernels/rmsnorm.py:21-46).
+   * sumsq_out: [M, ceil(N / 16)] FP32 out (STORE epilogue, 16-row tiles): element
+   *   [m, t] is the sum of the squares of the BF16 outputs y[m, 16 t .. 16 t + 15]
+   *   as stored (after the residual add of ftk_project_add_rows_bf16).
+   * sumsq: [M, K / 16] FP32 in (needs gamma; no residual, sum or x_ids): those sums
+   *   for x, as a call with sumsq_out wrote them; the prologue sums them (in a fixed
+   *   order) instead of reading x's rows. They must describe this x: nothing checks.
+   * Either one on a launch that is not RING (or sumsq_out not 16-row STORE) returns
+   * FTK_ERR_UNSUPPORTED. */
+  const float* sumsq;
+  float* sumsq_out;
 } ftk_rows;
 
 /* ftk_project_bf16 with the prologue's rows described by `rows` (NULL: x as is).
@@ -238,6 +253,12 @@ int ftk_project_rows_bf16(const void* x, const ftk_rows* rows, const void* gamma
  * of rmsnorm.py:98-125. cfg may be NULL. */
 int ftk_project_add_bf16(const void* x, const void* w, const void* residual, void* y, int64_t M, int64_t N,
                          int64_t K, const ftk_config* cfg, void* stream);
+
+/* ftk_project_add_bf16 that also writes rows->sumsq_out (the only field it takes; rows may be
+ * NULL): the residual stream's sums of squares for the norm that reads it next. Returns
+ * FTK_ERR_UNSUPPORTED, launching nothing, where the launch is not a 16-row RING tile. */
+int ftk_project_add_rows_bf16(const void* x, const ftk_rows* rows, const void* w, const void* residual, void* y,
+                              int64_t M, int64_t N, int64_t K, const ftk_config* cfg, void* stream);
 
 /* ---- standalone operators ---------------------------------------------------- */
 

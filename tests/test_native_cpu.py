@@ -125,6 +125,29 @@ def test_invalid_arguments_rejected_before_any_launch():
         rows = _native.Rows(None, None, fake, 8, table_rows)
         assert lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), fake, 1e-6, fake, ctypes.c_void_p(1 << 20), 1, 64,
                                          64, 0, None, 0, None, None, 0, None, None) == _native.FTK_ERR_INVALID
+    # the norm's sums of squares: sumsq feeds a norm (gamma) that reads x as it is; sumsq_out is
+    # written by the STORE epilogue, 4-byte aligned, clear of the call's other buffers
+    sq, y = ctypes.c_void_p(1 << 24), ctypes.c_void_p(1 << 20)
+
+    def rows_call(rows, gamma, epi=0):
+        return lib.ftk_project_rows_bf16(fake, ctypes.byref(rows), gamma, 1e-6, fake, y, 8, 64, 64, epi, None, 0,
+                                         None, None, 0, None, None)
+
+    assert rows_call(_native.Rows(None, None, None, 0, 0, sq, None), None) == _native.FTK_ERR_INVALID
+    assert rows_call(_native.Rows(buf, None, None, 0, 0, sq, None), fake) == _native.FTK_ERR_INVALID
+    assert rows_call(_native.Rows(None, None, fake, 8, 16, sq, None), fake) == _native.FTK_ERR_INVALID
+    assert rows_call(_native.Rows(None, None, None, 0, 0, ctypes.c_void_p((1 << 24) + 8), None), fake) \
+        == _native.FTK_ERR_UNSUPPORTED  # sums read in 16-byte pieces
+    assert rows_call(_native.Rows(None, None, None, 0, 0, None, sq), None, _native.EPI_SWIGLU) \
+        == _native.FTK_ERR_UNSUPPORTED
+    assert rows_call(_native.Rows(None, None, None, 0, 0, None, ctypes.c_void_p((1 << 24) + 2)), None) \
+        == _native.FTK_ERR_INVALID
+    assert rows_call(_native.Rows(None, None, None, 0, 0, None, ctypes.c_void_p((1 << 20) + 64)), None) \
+        == _native.FTK_ERR_INVALID  # inside y
+    # the residual-add form takes sumsq_out only
+    for rows in (_native.Rows(buf, None, None, 0, 0, None, sq), _native.Rows(None, None, None, 0, 0, sq, None)):
+        assert lib.ftk_project_add_rows_bf16(x, ctypes.byref(rows), w, r, y, 1, 64, 64, None, None) \
+            == _native.FTK_ERR_INVALID
     assert lib.ftk_embed_rms_norm_bf16(fake, 3, fake, fake, fake, fake, 1, 8, 1e-6, None) == _native.FTK_ERR_INVALID
     # the streaming-read reference: whole 16-byte chunks, an aligned source, a sink, a built window
     assert lib.ftk_stream_read(fake, 24, fake, 1, 4, None) == _native.FTK_ERR_INVALID
