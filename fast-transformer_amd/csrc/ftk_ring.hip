@@ -34,9 +34,9 @@
 //     order), reads it into registers, refills the slot, then runs the unit's
 //     arithmetic. No other wave touches those slots, so the main loop has no
 //     barrier.
-//   * x rows past M re-read row M - 1 (in bounds); rows past 4 NX are not read
-//     (their B operand is zero). Either way they feed only MFMA output columns
-//     >= M, which are never stored.
+//   * x rows past M re-read row M - 1 (in bounds); rows past 4 NX are not loaded:
+//     their lanes read the unit's first x slot. Either way they feed only MFMA
+//     output columns >= M, which are never stored (nor summed, nor compared).
 //   * With C <= 4 the first tile's B operands (normalised, with the prologue)
 //     stay in registers and later tiles load weights only, into 4 KiB slots:
 //     a wave's 16 KiB then hold all four units of the next tile in flight
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     for (int s = 0; s < 4; ++s) {
       u32x4_t b;
       if (fresh) {
-        b = x_real ? op[XO + s] : u32x4_t{0u, 0u, 0u, 0u};
+        b = op[XO + s];
         if constexpr (PRO) b = norm8(b, op[XO + 4 + s], scale);
         if constexpr (XREG) xr[j][s] = b;
       } else {
