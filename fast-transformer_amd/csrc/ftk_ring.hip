@@ -362,37 +362,34 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
               if (n0 + r < a.N) yr[n0 + r] = (uint16_t)bits[r];
           }
         }
+        if constexpr (EPI == EPI_STORE && RT == 16) {
+          if (a.sumsq_out != nullptr) {  // the entry's sum of squares waits in the slot it came from
+            const float v0 = bf16_to_f32(bits[0]), v1 = bf16_to_f32(bits[1]);
+            const float v2 = bf16_to_f32(bits[2]), v3 = bf16_to_f32(bits[3]);
+            part[i][0][0][ln][0] = (v0 * v0 + v1 * v1) + (v2 * v2 + v3 * v3);
+          }
+        }
         if constexpr (EPI == EPI_ARGMAX) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (n0 + r < a.N) best = key_max(best, argmax_key(bf16_to_f32(bits[r]), (uint32_t)(n0 + r)));
         }
       }
-      // The stored rows' sums of squares by tile (16 outputs), when asked: the same
-      // values again (the parked sums and the residual), squared and summed over the
-      // wave's lanes ln, ln + 16, ln + 32, ln + 48 (every lane of a wave takes the
-      // same entries of this loop: 64 per tile).
+      // The stored rows' sums of squares by tile (16 outputs), when asked: each entry's
+      // four squares (left in its parked slot above, by the same lane) summed over the
+      // wave's lanes ln, ln + 16, ln + 32, ln + 48 by two lane-half swaps, in the order
+      // (0 + 1) + (2 + 3). Every lane of a wave takes the same entries here (64 per tile).
       if constexpr (EPI == EPI_STORE && RT == 16) {
         if (a.sumsq_out != nullptr) {
           for (int e = tid; e < entries; e += 64 * KW) {
             const int ln = e & 63, i = e >> 6;
             const int ll = ln & 15, gg = ln >> 4;
-            const int tl = tile_at(done + i);
-            float sq = 0.f;
-            if (ll < M) {
-              f32x4_t s = part[i][0][0][ln];
-#pragma unroll
-              for (int w = 1; w < KW; ++w) s += part[i][w][0][ln];
-              const int n0 = tl * 16 + 4 * gg;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const float v = n0 + r < a.N ? bf16_to_f32(store_bits(a, s[r], ll, n0 + r)) : 0.f;
-                sq += v * v;
-              }
-            }
-            sq += __shfl_xor(sq, 16);
-            sq += __shfl_xor(sq, 32);
-            if (gg == 0 && ll < M) a.sumsq_out[(size_t)ll * ((a.N + 15) / 16) + tl] = sq;
+            const uint32_t sq = __float_as_uint(ll < M ? part[i][0][0][ln][0] : 0.f);
+            const auto r16 = __builtin_amdgcn_permlane16_swap(sq, sq, false, false);
+            const uint32_t pair = __float_as_uint(__uint_as_float(r16[0]) + __uint_as_float(r16[1]));
+            const auto r32 = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
+            const float total = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+            if (gg == 0 && ll < M) a.sumsq_out[(size_t)ll * ((a.N + 15) / 16) + tile_at(done + i)] = total;
           }
         }
       }
