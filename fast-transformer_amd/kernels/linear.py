@@ -98,7 +98,7 @@ class SumSq:
         need = y.shape[0] * ((y.shape[1] + 15) // 16)
         buf = self._buf
         if buf is None or buf.device != y.device or buf.numel() < need:
-            if torch.cuda.is_current_stream_capturing():
+            if y.is_cuda and torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("SumSq buffers must be sized during eager warmup, before graph capture")
             if buf is not None:
                 _native._RETIRED.append(buf)  # a captured graph may hold its address

@@ -12,7 +12,7 @@ Checked at 5, 8 and 16 rows (the RING kind's rows) at Qwen3-8B widths:
 - the rules that keep stale sums out: an in-place change of the rows, another tensor, a producer
   launch that is not RING;
 - a captured two-layer chain passing the sums along, replayed three times with eager work in
-  between, equal to the eager chain every time.
+  between, equal to the eager chain every time; a sums buffer first needed under capture raises.
 """
 
 import numpy as np
@@ -185,3 +185,17 @@ def test_captured_chain_replays_equal_eager(cuda, weights):
         assert torch.equal(out, want), f"replay {i}"
         L.linear(attn, w["o"])  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_a_buffer_first_needed_under_capture_raises(cuda, weights):
+    act = seeded((5, I), seed=8800, device=cuda)
+    L.linear_sumsq(act, weights["down"], L.SumSq())  # the shape itself warmed eagerly
+    fresh = L.SumSq()  # its buffer would be allocated inside the graph
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="eager warmup"):
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                L.linear_sumsq(act, weights["down"], fresh)
+    torch.cuda.synchronize()
