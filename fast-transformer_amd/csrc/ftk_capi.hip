@@ -205,8 +205,9 @@ static StageDefault stage_default(int64_t M, int epi, bool pro, int64_t N, int64
 
 // RING launch shape: 8 waves split K; two units in flight, three for the long K
 // (K = 12288) at up to 8 rows, where they fit the LDS.
-// lm_head + argmax (thousands of tiles) walks them in two rounds of workgroups:
-// 186.6 us at 5 rows against 188.7 with one round (and 188.3-189.0 for STAGE).
+// lm_head + argmax (thousands of tiles) walks them in one round of workgroups whose
+// last eighth of the tiles is claimed (ring_kernel's tail): 179.2 us per graph node
+// at 5 rows on MI355X, against 185.5 in the static two rounds used before.
 // Rows per tile (STORE): the fewest rows on the busiest CU, 16 first, then 12.
 // Where 16-row tiles leave a partial round of workgroups (N = 6144 on 256 CUs:
 // 384 tiles, so 192 workgroups walk two each), 12-row tiles fill every CU with
@@ -225,7 +226,9 @@ static int ring_busiest_rows(int tiles, int rt, int units) {
 static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K, int cus) {
   if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0, 0};
   const int c = quad_segments((int)K, 8);
-  const int gpc = epi == FTK_EPI_ARGMAX ? 2 : 1;
+  // One workgroup per CU, all resident: long walks claim their last tiles
+  // (ring_kernel), so workgroups that run ahead take more of them.
+  const int gpc = 1;
   int rows = 16;
   if (epi == FTK_EPI_STORE && ring_supported((int)M, (int)K, 8, 2, epi, pro, 12) &&
       ring_busiest_rows(ring_tiles(epi, (int)N, 12), 12, gpc * cus) <
@@ -419,7 +422,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     p->threads = 64 * kw;
     p->tiles = ring_tiles(epi, (int)N, rows);
     // One workgroup per CU at a time (its LDS fills the CU), each walking its
-    // share; lm_head + argmax in two rounds.
+    // share (the last tiles claimed, with a workspace).
     const int64_t units = (int64_t)(cfg && cfg->groups_per_cu ? cfg->groups_per_cu : (d.groups_per_cu ? d.groups_per_cu : 1)) * cus;
     p->grid = persistent_programs(p->tiles, (int)(units < p->tiles ? units : p->tiles));
     // A grid that is a multiple of 8 lets ring_tile give each XCD one contiguous
@@ -429,6 +432,10 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     const int even = (p->grid + 7) / 8 * 8;
     if (even <= p->tiles) p->grid = even;
     p->workspace_bytes = epi == FTK_EPI_ARGMAX ? argmax_keys_bytes(p->grid, M) : 0;
+    // The claims of long walks (without a workspace the walk keeps its static order
+    // throughout).
+    if (p->tiles >= kRingTailMinTiles * p->grid && p->workspace_bytes < kWsClaim + 4)
+      p->workspace_bytes = kWsClaim + 4;
     return FTK_OK;
   }
   if (kind == FTK_KIND_MFMA_STREAM) {
@@ -813,6 +820,10 @@ static int project_impl(const void* x, const ftk_rows* rows, const void* gamma, 
   if (r.sumsq_out != nullptr && (p.kind != FTK_KIND_RING || p.rows_per_wave != 16)) return FTK_ERR_UNSUPPORTED;
   a.sumsq = r.sumsq;
   a.sumsq_out = r.sumsq_out;
+  // Long RING walks claim their last tiles from the workspace's counter.
+  if (p.kind == FTK_KIND_RING && p.tiles >= kRingTailMinTiles * p.grid && workspace != nullptr &&
+      workspace_bytes >= kWsClaim + 4)
+    a.claim = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) + kWsClaim);
   char* ws = (char*)workspace;
   if (epilogue == FTK_EPI_ARGMAX) a.keys = (unsigned long long*)(ws + kWsKeys);
   // Greedy argmax in one launch (argmax_gather) for the STREAM kind: one row, or at most one key

@@ -47,6 +47,10 @@ struct ProjArgs {
   // its x) sums those parts instead of reading the rows of x.
   const float* sumsq;
   float* sumsq_out;
+  // Long RING walks (kRingTailMinTiles or more tiles per workgroup): the counter their
+  // last tiles are claimed from (zero between calls; the launch's last claim resets
+  // it), or null for the static order throughout.
+  unsigned* claim;
 };
 
 // The BF16 bits a STORE epilogue writes for output (m, n) with FP32 sum s.

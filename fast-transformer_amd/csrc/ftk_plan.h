@@ -224,6 +224,12 @@ FTK_HD constexpr int ring_max_depth(int c, int kw, int d, int nx, bool pro, int 
 // allocated, and whichever reads the keys (the finalize launch, or the gathering
 // workgroup of the one-launch argmax) zeroes each word it has read.
 constexpr int64_t kWsScale = 0;     // [32] f32 RMSNorm row scales (MFMA kind)
+constexpr int64_t kWsClaim = 128;   // u32 tail-tile claims of a RING launch (zero between calls)
+// RING walks of at least this many tiles per workgroup claim their last tiles (the
+// tail) from kWsClaim: lm_head + argmax at 5 rows 185.5 -> 179.2 us per graph node on
+// MI355X. Shorter walks keep the static order (gate/up's six tiles: 32.8 -> 34.3 us
+// claimed; its claims crowd into the walks' last tile).
+constexpr int kRingTailMinTiles = 16;
 constexpr int64_t kWsKeys = 256;    // [grid][M] u64 per-workgroup greedy-argmax keys
 
 // Persistent launch: the fewest programs that keep the deepest walk at

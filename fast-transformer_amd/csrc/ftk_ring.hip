@@ -136,6 +136,24 @@ __device__ __forceinline__ float lds_read_f32(const float* p) {
   return v;
 }
 
+__device__ __forceinline__ void lds_write_u32(uint32_t* p, uint32_t v) {
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)p;
+  asm volatile("ds_write_b32 %0, %1" ::"v"(at), "v"(v) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_read_u32(const uint32_t* p) {
+  uint32_t v;
+  const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)p;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(at) : "memory");
+  return v;
+}
+// An agent-scope atomic add returning the old value, as assembly: the compiler does
+// not count it, so it adds no wait of its own; the walk's exact waits return it.
+__device__ __forceinline__ uint32_t claim_add(unsigned* p) {
+  uint32_t old;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(old) : "v"(p), "v"(1u) : "memory");
+  return old;
+}
+
 // Workgroup barrier for LDS traffic only. __syncthreads() also waits for every
 // vector memory operation (vmcnt(0)), which would empty the ring mid-walk.
 __device__ __forceinline__ void lds_barrier() {
@@ -154,7 +172,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 }  // namespace
 
-template <int C, int KW, int D, int NX, bool PRO, int EPI, int RT>
+template <int C, int KW, int D, int NX, bool PRO, int EPI, int RT, bool TAIL = false>
 __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   static_assert(C % D == 0, "a tile's units must fill the ring exactly");
   static_assert(NX == 2 || NX == 4, "x rows per unit: 8 or 16");
@@ -180,8 +198,71 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
   const int li = lane & 15, g = lane >> 4;  // MFMA layout: row li, k quarter g
   const int M = a.M, K = a.K;               // K == 128 C KW (checked by the planner)
   const int wg = blockIdx.x, G = gridDim.x;
-  const int my_tiles = (tiles - wg + G - 1) / G;  // steps of this workgroup (grid <= tiles)
-  auto tile_at = [&](int i) { return ring_tile(wg, i, G, tiles); };
+  // Claimed tail (TAIL builds, given a.claim; register-held B operands and
+  // kRingTailMinTiles or more tiles per workgroup): the first `rounds` positions of workgroup wg's walk are its static
+  // tiles (ring_tile over rounds * G tiles); the rest of the tiles, the tail, are
+  // claimed from *a.claim (the c-th claim of the launch is tile rounds * G + c; a
+  // claim past the tail ends the walk), so the workgroups that run ahead take more of
+  // them. Wave 0 claims position k + 2 at the top of position k, before it issues the
+  // units of position k + 1: loads complete in order, so the wait for position
+  // k + 1's first unit returns the claim too. It publishes each claimed tile in
+  // seq_lds (slot k % 16, tagged with the position); the other waves read it there,
+  // waiting for the tag while wave 0 is behind (no barrier lies between, so wave 0
+  // never waits for them on the way). Every walk ends with exactly one claim past
+  // the tail, so the launch's last claim finds the counter at tail + G - 1 and puts
+  // it back to zero.
+  const int per = tiles / G;
+  const bool dyn = TAIL && XREG && per >= kRingTailMinTiles;  // uniform
+  const int rounds = dyn ? per - per / 8 : 0;  // the tail: about an eighth of the tiles
+  const int static_tiles = dyn ? rounds * G : tiles, tail = tiles - static_tiles;
+  const int my_tiles = (static_tiles - wg + G - 1) / G;  // static steps of this workgroup (grid <= tiles)
+  auto tile_at = [&](int i) { return ring_tile(wg, i, G, static_tiles); };
+  __shared__ uint32_t seq_lds[16];
+  uint32_t claim_v = 0;  // wave 0, lane 0: the claim in flight
+  auto seq_word = [](int k, int tile) { return ((uint32_t)(k & 0xFFF) << 20) | (uint32_t)(tile + 1); };
+  // Tile of position k (-1 past the walk's end), once published.
+  auto walk_tile = [&](int k) {
+    if (!dyn) return k < my_tiles ? tile_at(k) : -1;
+    if (k < rounds) return tile_at(k);
+    const uint32_t want = (uint32_t)(k & 0xFFF) << 20;
+    uint32_t v = lds_read_u32(&seq_lds[k & 15]);
+    while ((v & 0xFFF00000u) != want) {
+      __builtin_amdgcn_s_sleep(1);
+      v = lds_read_u32(&seq_lds[k & 15]);
+    }
+    return (int)(v & 0xFFFFFu) - 1;
+  };
+  // At the top of position k (its first unit's wait done): publish position k + 1
+  // if it was claimed (the wait returned its claim), claim position k + 2 if it lies
+  // in the tail and the walk goes on. Returns the tile of position k + 1.
+  auto advance = [&](int k) {
+    if (dyn && kw == 0 && k + 2 >= rounds) {
+      if (k + 1 >= rounds) asm volatile("" : "+v"(claim_v));  // returned by the wait before this
+      if (lane == 0) {
+        bool go = true;
+        if (k + 1 >= rounds) {
+          const int c = (int)claim_v;
+          const int next = c < tail ? static_tiles + c : -1;
+          lds_write_u32(&seq_lds[(k + 1) & 15], seq_word(k + 1, next));
+          go = next >= 0;
+          if (!go && c == tail + G - 1) __hip_atomic_store(a.claim, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (go) claim_v = claim_add(a.claim);
+      }
+    }
+    return walk_tile(k + 1);
+  };
+  // The tile of a parked position (static builds: the static order).
+  auto flush_tile = [&](int k) {
+    if constexpr (TAIL) return walk_tile(k);
+    else return tile_at(k);
+  };
+  if constexpr (TAIL) {
+    // Slot s starts with the tag of position s - 16 (never read: each slot is written
+    // before its position is read); the barrier before the walk (the prologue's, or
+    // the one after the first units) orders these writes first.
+    if (dyn && kw == 0 && lane < 16) lds_write_u32(&seq_lds[lane], seq_word(lane - 16, -1));
+  }
   const int outputs = gemv_outputs(EPI, a.N);
 
   // ---- where this lane's loads go -------------------------------------------
@@ -257,8 +338,12 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 
   // ---- the first D units (all of the first tile: D <= C) ----------------------
   asm volatile("" ::: "memory");  // keep the prologue's loads ahead of the units (the count below)
+  const int tile0 = tile_at(0);
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(tile_at(0), d, ring[kw] + d * SLOT, true);
+  for (int d = 0; d < D; ++d) issue(tile0, d, ring[kw] + d * SLOT, true);
+  if constexpr (TAIL && !PRO) {
+    if (dyn) lds_barrier();  // the tail's slots are written
+  }
 
   // ---- RMSNorm prologue, part 2: row scales while the first units stream -------
   float scale = 0.f;
@@ -317,7 +402,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
       for (int e = tid; e < entries; e += 64 * KW) {
         const int ll = e & 15, h = (e >> 4) & 1, i = e >> 5;
         if (ll >= M) continue;
-        const int tl = tile_at(done + i);
+        const int tl = flush_tile(done + i);
         f32x4_t s = part[i][0][0][h * 16 + ll];
         f32x4_t u = part[i][0][0][(2 + h) * 16 + ll];
 #pragma unroll
@@ -339,7 +424,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
         const int ln = e & 63, sub = (e >> 6) % SUB, i = e / (64 * SUB);
         const int ll = ln & 15, gg = ln >> 4;
         if (ll >= M || 16 * sub + 4 * gg >= RT) continue;
-        const int tl = tile_at(done + i);
+        const int tl = flush_tile(done + i);
         f32x4_t s = part[i][0][sub][ln];
 #pragma unroll
         for (int w = 1; w < KW; ++w) s += part[i][w][sub][ln];
@@ -389,7 +474,7 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
             const uint32_t pair = __float_as_uint(__uint_as_float(r16[0]) + __uint_as_float(r16[1]));
             const auto r32 = __builtin_amdgcn_permlane32_swap(pair, pair, false, false);
             const float total = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-            if (gg == 0 && ll < M) a.sumsq_out[(size_t)ll * ((a.N + 15) / 16) + tile_at(done + i)] = total;
+            if (gg == 0 && ll < M) a.sumsq_out[(size_t)ll * ((a.N + 15) / 16) + flush_tile(done + i)] = total;
           }
         }
       }
@@ -465,48 +550,108 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
     // slots q0..q3 (RT / 4 KiB each) and the next tile's units go there, all four
     // in flight: those wholly inside slot 0 (q0, and q1 too with 16 x rows) once
     // slot 0 is free, the rest once slot 1 is.
-    const bool more0 = my_tiles > 1;
-    f32x4_t acc[SUB] = {};
-    static_for<0, C>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      constexpr int early = SLOT / WS;  // next-tile units issued after unit C - 2
-      if constexpr (j < C - 1) {
-        wait_vm<WL + NX>();
-      } else {
-        if (more0) wait_vm<WL * early>(); else wait_vm<0>();
-      }
-      unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
-        if constexpr (j + 2 < C) {
-          issue(tile_at(0), j + 2, ring[kw] + (j % 2) * SLOT, true);
-        } else if constexpr (j == C - 2) {
-          if (more0) {
-#pragma unroll
-            for (int q = 0; q < early; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
-          }
+    if constexpr (TAIL) {
+      int tile1 = dyn ? -1 : walk_tile(1);
+      bool more0 = tile1 >= 0;
+      f32x4_t acc[SUB] = {};
+      static_for<0, C>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        constexpr int early = SLOT / WS;  // next-tile units issued after unit C - 2
+        if constexpr (j < C - 1) {
+          wait_vm<WL + NX>();
         } else {
-          if (more0) {
-#pragma unroll
-            for (int q = early; q < 4; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
+          if (more0) wait_vm<WL * early>(); else wait_vm<0>();
+        }
+        if constexpr (j == 0) {
+          if (dyn) {
+            tile1 = advance(0);
+            more0 = tile1 >= 0;
           }
         }
-      });
-    });
-    if (park(acc, more0)) {
-      // Later tiles: unit j of tile i sits in q_j; after reading it, unit j of
-      // tile i + 1 takes its place, so the next tile is in flight in full.
-      for (int i = 1; i < my_tiles; ++i) {
-        const int tile_next = tile_at(i + 1);
-        const bool more = i + 1 < my_tiles;
-        f32x4_t acc2[SUB] = {};
-        static_for<0, C>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
-          if (more) wait_vm<WL * (C - 1)>(); else wait_vm<WL * (C - 1 - j)>();
-          unit(ring[kw] + WS * j, J, false, acc2, [&] {
-            if (more) issue(tile_next, j, ring[kw] + WS * j, false);
-          });
+        unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
+          if constexpr (j + 2 < C) {
+            issue(tile0, j + 2, ring[kw] + (j % 2) * SLOT, true);
+          } else if constexpr (j == C - 2) {
+            if (more0) {
+  #pragma unroll
+              for (int q = 0; q < early; ++q) issue(tile1, q, ring[kw] + WS * q, false);
+            }
+          } else {
+            if (more0) {
+  #pragma unroll
+              for (int q = early; q < 4; ++q) issue(tile1, q, ring[kw] + WS * q, false);
+            }
+          }
         });
-        if (!park(acc2, more)) break;
+      });
+      if (park(acc, more0)) {
+        // Later tiles: unit j of tile i sits in q_j; after reading it, unit j of
+        // tile i + 1 takes its place, so the next tile is in flight in full.
+        for (int i = 1; dyn || i < my_tiles; ++i) {
+          int tile_next = dyn ? -1 : walk_tile(i + 1);
+          bool more = dyn || tile_next >= 0;
+          f32x4_t acc2[SUB] = {};
+          static_for<0, C>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
+            if (more) wait_vm<WL * (C - 1)>(); else wait_vm<WL * (C - 1 - j)>();
+            if constexpr (j == 0) {
+              if (dyn) {
+                tile_next = advance(i);
+                more = tile_next >= 0;
+              }
+            }
+            unit(ring[kw] + WS * j, J, false, acc2, [&] {
+              if (more) issue(tile_next, j, ring[kw] + WS * j, false);
+            });
+          });
+          if (!park(acc2, more)) break;
+        }
+      }
+    } else {
+      const bool more0 = my_tiles > 1;
+      f32x4_t acc[SUB] = {};
+      static_for<0, C>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        constexpr int early = SLOT / WS;  // next-tile units issued after unit C - 2
+        if constexpr (j < C - 1) {
+          wait_vm<WL + NX>();
+        } else {
+          if (more0) wait_vm<WL * early>(); else wait_vm<0>();
+        }
+        unit(ring[kw] + (j % 2) * SLOT, J, true, acc, [&] {
+          if constexpr (j + 2 < C) {
+            issue(tile_at(0), j + 2, ring[kw] + (j % 2) * SLOT, true);
+          } else if constexpr (j == C - 2) {
+            if (more0) {
+  #pragma unroll
+              for (int q = 0; q < early; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
+            }
+          } else {
+            if (more0) {
+  #pragma unroll
+              for (int q = early; q < 4; ++q) issue(tile_at(1), q, ring[kw] + WS * q, false);
+            }
+          }
+        });
+      });
+      if (park(acc, more0)) {
+        // Later tiles: unit j of tile i sits in q_j; after reading it, unit j of
+        // tile i + 1 takes its place, so the next tile is in flight in full.
+        for (int i = 1; i < my_tiles; ++i) {
+          const int tile_next = tile_at(i + 1);
+          const bool more = i + 1 < my_tiles;
+          f32x4_t acc2[SUB] = {};
+          static_for<0, C>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            // issued after unit j: units j+1..3 of this tile and units 0..j-1 of the next
+            if (more) wait_vm<WL * (C - 1)>(); else wait_vm<WL * (C - 1 - j)>();
+            unit(ring[kw] + WS * j, J, false, acc2, [&] {
+              if (more) issue(tile_next, j, ring[kw] + WS * j, false);
+            });
+          });
+          if (!park(acc2, more)) break;
+        }
       }
     }
   } else {
@@ -552,6 +697,15 @@ __global__ __launch_bounds__(64 * KW) void ring_kernel(ProjArgs a, int tiles) {
 // ---- dispatch -------------------------------------------------------------------
 
 typedef void (*RingKernel)(ProjArgs, int);
+
+// Claimed-tail builds: lm_head + argmax with the norm (the walks long enough, at
+// kRingTailMinTiles tiles per workgroup, are the vocabulary's).
+static RingKernel pick_ring_tail(int c, int kw, int d, int nx, int rt, bool pro, int epi) {
+  if (epi != EPI_ARGMAX || !pro || c != 4 || kw != 8 || d != 2 || rt != 16) return nullptr;
+  if (nx == 2) return ring_kernel<4, 8, 2, 2, true, EPI_ARGMAX, 16, true>;
+  if (nx == 4) return ring_kernel<4, 8, 2, 4, true, EPI_ARGMAX, 16, true>;
+  return nullptr;
+}
 
 // Instantiated (C, KW, D, NX, RT): K = 4096 (C = 4 at 8 waves, with or without the
 // prologue, every epilogue) with two units in flight, and 24-row tiles for the
@@ -599,8 +753,10 @@ bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows
 
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& sh, hipStream_t stream) {
   const int c = quad_segments(a.K, sh.kw);
-  RingKernel k =
-      c > 0 ? pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi) : nullptr;
+  RingKernel k = nullptr;
+  if (c > 0 && a.claim != nullptr)
+    k = pick_ring_tail(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi);
+  if (k == nullptr && c > 0) k = pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi);
   if (k == nullptr || a.M < 2 || a.M > kRingMaxRows) return hipErrorInvalidValue;
   if (sh.grid < 1 || sh.grid > sh.tiles) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(sh.grid), dim3(64 * sh.kw), 0, stream, a, sh.tiles);

@@ -20,20 +20,24 @@
  *   - M (rows of x) is 1..FTK_MAX_ROWS, as the reference's MAX_ROWS = 32
  *     (engine/kernels/linear.py:343); larger M is the caller's native GEMM.
  *   - Workspaces hold per-call scratch (RMSNorm row scales, per-workgroup
- *     argmax keys). Zero a workspace once when it is allocated: the argmax key
- *     words (from byte 256) must be zero when a call starts, and every call
- *     leaves the ones it used zero again (the one-launch argmax reads a
- *     non-zero word as a key of the current call). Nothing else carries over
- *     between calls. Calls that share a workspace must not run concurrently.
- *     (The norm's row sums of ftk_rows.sumsq_out / sumsq are the caller's own
- *     buffer, written by one call for a later one to read.)
- *   - No kernel uses device-scope fences or tickets. One workgroup waits on
- *     others: the extra, last workgroup of a one-launch lm_head + argmax (the
- *     STREAM kind, M = 1) reads the other workgroups' key words, with a
- *     bounded wait (1 s; then the row's id is -1). The others never wait, so
- *     its wait ends in whatever order the workgroups run. After an id of -1
- *     the workspace may hold that call's late key words: zero it again before
- *     the next call.
+ *     argmax keys, a tile-claim counter). Zero a workspace once when it is
+ *     allocated: the argmax key words (from byte 256) and the claim counter
+ *     (bytes 128..131) must be zero when a call starts, and every call leaves
+ *     them zero again (the one-launch argmax reads a non-zero word as a key of
+ *     the current call; the counter's last claim puts it back). Nothing else
+ *     carries over between calls. Calls that share a workspace must not run
+ *     concurrently. (The norm's row sums of ftk_rows.sumsq_out / sumsq are the
+ *     caller's own buffer, written by one call for a later one to read.)
+ *   - No kernel uses device-scope fences. The RING kind's long walks (lm_head
+ *     + argmax at 5..16 rows) claim their last tiles with agent-scope atomic
+ *     adds on the workspace's counter; a workspace smaller than
+ *     ftk_project_workspace_bytes() (or none, where no argmax needs one) keeps
+ *     those walks in their static order. One workgroup waits on others: the
+ *     extra, last workgroup of a one-launch lm_head + argmax (the STREAM kind,
+ *     M = 1) reads the other workgroups' key words, with a bounded wait (1 s;
+ *     then the row's id is -1). The others never wait, so its wait ends in
+ *     whatever order the workgroups run. After an id of -1 the workspace may
+ *     hold that call's late key words: zero it again before the next call.
  */
 #ifndef FTK_H
 #define FTK_H

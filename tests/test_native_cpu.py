@@ -419,10 +419,12 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_RING and p.waves == 8 and p.unroll == 3
     _native.call("ftk_plan_project", 8, 24576, 4096, _native.EPI_SWIGLU | _native.PLAN_PROLOGUE, 256, None, p)
     assert p.kind == _native.KIND_RING and p.tiles == 12288 // 8 and p.grid == 256
+    assert p.workspace_bytes == 0  # six tiles per walk: the static order, no claims
     _native.call("ftk_plan_project", 16, 4096, 12288, 0, 256, None, p)  # 16 x rows: two units fit
     assert p.kind == _native.KIND_RING and p.unroll == 2
     _native.call("ftk_plan_project", 5, 151936, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
-    assert p.kind == _native.KIND_RING and p.tiles == 9496 and p.grid == 504  # lm_head: two rounds, 8 | grid
+    # lm_head: one round (8 | grid), 37 tiles per walk, the last eighth claimed from the workspace
+    assert p.kind == _native.KIND_RING and p.tiles == 9496 and p.grid == 256 and p.workspace_bytes >= 256 + 256 * 5 * 8
     # the prologue's residual add is not a RING form: such calls plan as before
     _native.call("ftk_plan_project", 5, 6144, 4096, _native.PLAN_PROLOGUE | _native.PLAN_RESIDUAL, 256, None, p)
     assert p.kind == _native.KIND_QUAD
