@@ -646,8 +646,8 @@ def profile_kernels(dev, passes=2):
     defaults (for rocprofv3 counter runs), in the order of PROFILE_KERNELS, then a 1 GiB copy as the
     counter reference. All weights are made first, so the projection launches are the only ftk
     dispatches, ``passes`` times each: C3's 36 layers (QKV, O, gate/up + SwiGLU, down), C5's lm_head
-    + argmax at M = 1 and 5 over C5_COPIES weight copies (at M = 1 one launch that also gathers the
-    ids; at M = 5 the projection, then the argmax finalize),
+    + argmax at M = 1 and 5 over C5_COPIES weight copies (at both the RING projection, whose walks
+    end in claimed tiles, then the argmax finalize),
     C2's 28 layers, C1's QKV projection without the norm over 64 weight copies."""
     L.TUNE = False
     model8 = Model(QWEN3_8B, dev, head=True)

@@ -224,7 +224,7 @@ static int ring_busiest_rows(int tiles, int rt, int units) {
   return grid > 0 ? (tiles + grid - 1) / grid * rt : 0;
 }
 static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t K, int cus) {
-  if (M < 2 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0, 0};
+  if (M < 1 || M > kRingMaxRows || K > INT32_MAX || N > INT32_MAX) return {0, 0, 0, 0};
   const int c = quad_segments((int)K, 8);
   // One workgroup per CU, all resident: long walks claim their last tiles
   // (ring_kernel), so workgroups that run ahead take more of them.
@@ -239,11 +239,18 @@ static RingDefault ring_default(int64_t M, int epi, bool pro, int64_t N, int64_t
     if (ring_supported((int)M, (int)K, d.kw, d.depth, epi, pro, d.rows)) return d;
   return {0, 0, 0, 0};
 }
-// Where RING beats the other kinds (MI355X, Qwen3-8B shapes, 5..16 rows): every
-// projection, SwiGLU and lm_head + argmax, with or without the norm prologue.
+// Where RING beats the other kinds (MI355X, Qwen3-8B shapes): at 5..16 rows every
+// projection, SwiGLU and lm_head + argmax, with or without the norm prologue; at
+// 1..4 rows lm_head + argmax with the prologue where every workgroup walks enough
+// tiles for the claimed tail (151936 x 4096, per graph node: 177.7 us at M = 1
+// against STREAM's one launch, 184.4; 178.0 at M = 2 against QUAD, 187).
 // Not with the prologue's residual add, which RING does not take (project_impl
 // plans such calls without it).
-static bool ring_preferred(int64_t M, int epi) { (void)epi; return M >= 5; }
+static bool ring_preferred(int64_t M, int epi, bool pro, int64_t N, int64_t K, int cus) {
+  if (M >= 5) return true;
+  return epi == FTK_EPI_ARGMAX && M >= 1 && ring_tail_supported((int)M, (int)K, 8, 2, epi, pro, 16) &&
+         ring_tiles(epi, (int)N, 16) >= (int64_t)kRingTailMinTiles * cus;
+}
 
 constexpr int kMfmaDefaultUnroll = 4;
 constexpr int kMfmaDefaultWaves = 16;
@@ -263,14 +270,15 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
   if (epi == FTK_EPI_SWIGLU && (N % 2)) return FTK_ERR_INVALID;
   int kind = cfg && cfg->kind ? cfg->kind : FTK_KIND_AUTO;
   if (kind == FTK_KIND_AUTO) {
-    // Measured on MI355X at the Qwen3-8B shapes: STREAM (v_dot2) at M = 1 and
+    // Measured on MI355X at the Qwen3-8B shapes: RING (direct-to-LDS 16x16x32
+    // tiles) where ring_preferred says so; below that STREAM (v_dot2) at M = 1 and
     // up to M = 4; QUAD (4x4x4 MFMA blocks) where quad_preferred says so; STAGE
     // (16x16x32 via LDS) for the rest of M = 5..16; MFMA_STREAM where neither has
     // the shape.
     const bool quad = quad_default(M, epi, pro, N, K).rows != 0;
     const bool stage = M >= 5 && stage_default(M, epi, pro, N, K).t != 0;
-    const RingDefault rd = ring_ok && ring_preferred(M, epi) ? ring_default(M, epi, pro, N, K, cus)
-                                                              : RingDefault{0, 0, 0, 0};
+    const RingDefault rd = ring_ok && ring_preferred(M, epi, pro, N, K, cus) ? ring_default(M, epi, pro, N, K, cus)
+                                                                             : RingDefault{0, 0, 0, 0};
     // RING holds one workgroup per CU: where its tiles would leave more than half
     // the CUs idle and QUAD is preferred at these rows, QUAD's smaller tiles keep
     // more of them streaming (a Qwen3-8B eight-way tensor-parallel shard's QKV,
@@ -408,7 +416,7 @@ static int plan(int64_t M, int64_t N, int64_t K, int epi, int cus, const ftk_con
     return FTK_OK;
   }
   if (kind == FTK_KIND_RING) {
-    if (M < 2 || M > kRingMaxRows) return FTK_ERR_UNSUPPORTED;
+    if (M < 1 || M > kRingMaxRows) return FTK_ERR_UNSUPPORTED;
     const RingDefault d = ring_default(M, epi, pro, N, K, cus);
     const int kw = cfg && cfg->waves ? cfg->waves : (d.kw ? d.kw : 8);
     const int depth = cfg && cfg->unroll ? cfg->unroll : (d.depth ? d.depth : 2);

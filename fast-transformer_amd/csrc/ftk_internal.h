@@ -278,6 +278,8 @@ struct RingShape {
   int rows;      // RT: weight rows per tile (12, 16 or 24)
 };
 bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows = 16);
+// A build with the claimed tail exists for this shape (long walks of lm_head + argmax).
+bool ring_tail_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows);
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& shape, hipStream_t stream);
 
 // Launch shape of the MFMA kind.

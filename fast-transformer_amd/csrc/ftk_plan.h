@@ -153,7 +153,7 @@ constexpr bool quad_fits(int mq, int rs, int c, int kw, bool pro) {
 constexpr int kStageMaxRows = 16;
 FTK_HD constexpr int stage_max_depth(int t, int kw) { return (64 * 1024) / (t * kw * 1024); }
 
-// ---- M = 2..16 with K = 128 C KW: the RING kind (direct-to-LDS loads) --------
+// ---- M = 1..16 with K = 128 C KW: the RING kind (direct-to-LDS loads) --------
 // Segments as the QUAD kind (wave kw reads the 128-wide K segments j KW + kw).
 // A tile is RT weight rows: rows RT t .. RT t + RT - 1 (RT = 16, or 24 where 16-row
 // tiles would leave a partial round of workgroups, e.g. N = 6144 on 256 CUs), or

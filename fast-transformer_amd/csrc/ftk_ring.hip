@@ -1,4 +1,4 @@
-// M = 2..16 skinny BF16 projection, RING kind: weight and x segments land in a
+// M = 1..16 skinny BF16 projection, RING kind: weight and x segments land in a
 // per-wave LDS ring by direct-to-LDS loads (global_load_lds_dwordx4) and feed
 // 16x16x32 BF16 MFMAs (v_mfma_f32_16x16x32_bf16).
 //
@@ -8,7 +8,8 @@
 // greedy argmax engine/kernels/argmax.py:19-48), FP32 accumulation, one rounding.
 //
 // Why: at 5..16 rows the kernels that hold x in registers spend as many L2
-// requests on x as on the weights. An MFMA B operand needs x row l % 16 in lane
+// requests on x as on the weights. (Below 5 rows the planner takes this kind for
+// lm_head + argmax only, whose long walks end in the claimed tail.) An MFMA B operand needs x row l % 16 in lane
 // l, so a register load of it touches 16 rows x 64 bytes per wave instruction.
 // Here x travels like the weights, 4 rows x 256 contiguous bytes per wave
 // instruction, straight into LDS, and is read back in MFMA layout. The weight
@@ -747,8 +748,14 @@ static RingKernel pick_ring(int c, int kw, int d, int nx, int rt, bool pro, int 
 
 bool ring_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows) {
   const int c = quad_segments(K, kw);
-  return M >= 2 && M <= kRingMaxRows && c > 0 &&
+  return M >= 1 && M <= kRingMaxRows && c > 0 &&
          pick_ring(c, kw, depth, ring_x_loads(M), rows, pro, epi) != nullptr;
+}
+
+bool ring_tail_supported(int M, int K, int kw, int depth, int epi, bool pro, int rows) {
+  const int c = quad_segments(K, kw);
+  return M >= 1 && M <= kRingMaxRows && c > 0 &&
+         pick_ring_tail(c, kw, depth, ring_x_loads(M), rows, pro, epi) != nullptr;
 }
 
 hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& sh, hipStream_t stream) {
@@ -757,7 +764,7 @@ hipError_t launch_ring(const ProjArgs& a, int epi, const RingShape& sh, hipStrea
   if (c > 0 && a.claim != nullptr)
     k = pick_ring_tail(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi);
   if (k == nullptr && c > 0) k = pick_ring(c, sh.kw, sh.depth, ring_x_loads(a.M), sh.rows, a.gamma != nullptr, epi);
-  if (k == nullptr || a.M < 2 || a.M > kRingMaxRows) return hipErrorInvalidValue;
+  if (k == nullptr || a.M < 1 || a.M > kRingMaxRows) return hipErrorInvalidValue;
   if (sh.grid < 1 || sh.grid > sh.tiles) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(sh.grid), dim3(64 * sh.kw), 0, stream, a, sh.tiles);
   return hipGetLastError();

@@ -342,7 +342,7 @@ def _candidates(m, n, k, epilogue=_native.EPI_STORE, prologue=False):
             for kw in (4, 8):
                 for gpc in (1, 32):
                     configs.append((_native.KIND_QUAD, rows, 0, gpc, kw))
-    if 2 <= m <= 16:
+    if 2 <= m <= 16 or (m == 1 and epilogue == _native.EPI_ARGMAX):
         for rows in (12, 16, 24):
             for depth in (2, 3):
                 for gpc in (1, 2):

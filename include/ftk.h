@@ -29,12 +29,13 @@
  *     concurrently. (The norm's row sums of ftk_rows.sumsq_out / sumsq are the
  *     caller's own buffer, written by one call for a later one to read.)
  *   - No kernel uses device-scope fences. The RING kind's long walks (lm_head
- *     + argmax at 5..16 rows) claim their last tiles with agent-scope atomic
- *     adds on the workspace's counter; a workspace smaller than
- *     ftk_project_workspace_bytes() (or none, where no argmax needs one) keeps
- *     those walks in their static order. One workgroup waits on others: the
- *     extra, last workgroup of a one-launch lm_head + argmax (the STREAM kind,
- *     M = 1) reads the other workgroups' key words, with a bounded wait (1 s;
+ *     + argmax with the norm prologue, 1..16 rows) claim their last tiles with
+ *     agent-scope atomic adds on the workspace's counter; a workspace smaller
+ *     than ftk_project_workspace_bytes() (or none, where no argmax needs one)
+ *     keeps those walks in their static order. One workgroup waits on others:
+ *     the extra, last workgroup of a one-launch lm_head + argmax (the STREAM
+ *     kind at M = 1, the default where the RING kind's claimed tail does not
+ *     apply) reads the other workgroups' key words, with a bounded wait (1 s;
  *     then the row's id is -1). The others never wait, so its wait ends in
  *     whatever order the workgroups run. After an id of -1 the workspace may
  *     hold that call's late key words: zero it again before the next call.
@@ -89,7 +90,7 @@ typedef enum ftk_kind {
                                weights loaded as 4 rows x 256 contiguous bytes per wave load */
   FTK_KIND_STAGE = 7,       /* M <= 16, K = 128 C KW: QUAD's weight loads staged through LDS into
                                16x16x32 MFMA tiles */
-  FTK_KIND_RING = 8         /* M = 2..16, K = 128 C KW: weight and x segments loaded straight into a
+  FTK_KIND_RING = 8         /* M = 1..16, K = 128 C KW: weight and x segments loaded straight into a
                                per-wave LDS ring (global_load_lds_dwordx4), 16x16x32 MFMA tiles;
                                no residual-add prologue */
 } ftk_kind;
@@ -224,7 +225,7 @@ typedef struct ftk_rows {
                             device, so the device clamps them into the table: an id below 0 reads
                             row 0 and an id at or past x_rows reads row x_rows - 1 */
   /* The norm's statistics carried from the projection that writes a row stream to the
-   * norm that reads it (the RING kind, M = 2..16). No counterpart in the reference,
+   * norm that reads it (the RING kind, M = 1..16). No counterpart in the reference,
    * whose norm reads its input rows (engine/kernels/rmsnorm.py:21-46).
    * sumsq_out: [M, ceil(N / 16)] FP32 out (STORE epilogue, 16-row tiles): element
    *   [m, t] is the sum of the squares of the BF16 outputs y[m, 16 t .. 16 t + 15]

@@ -1,14 +1,15 @@
 """GPU tests of the one-launch greedy argmax (lm_head + argmax, engine/kernels/argmax.py:112-129).
 
-The STREAM kind (the M = 1 default) gathers the workgroups' keys in one extra workgroup of the
-projection launch; the other kinds keep the second, finalize launch. Both forms share the key region
-of the projection workspace, which is zero between calls. Checked here:
+The STREAM kind (at M = 1 the default without the norm prologue, or where RING's claimed tail does
+not apply) gathers the workgroups' keys in one extra workgroup of the projection launch; the other
+kinds keep the second, finalize launch. Both forms share the key region of the projection
+workspace, which is zero between calls. Checked here:
 - ids equal the first maximum of the kernel's own BF16 logits (and top equals that logit), through
   every kind in one sequence of calls sharing the workspace, and the key region is zero after each;
 - exact ties take the lowest index and a NaN logit wins, through the gathered form (M = 1) and the
   two-launch RING form (M = 5, 16) alike;
-- a captured graph of a gathered (M = 1) and a two-launch (M = 5) call replays to the eager ids
-  every time, with another two-launch call between the replays.
+- a captured graph of a gathered (STREAM, M = 1) and a two-launch (M = 5) call replays to the
+  eager ids every time, with another two-launch call between the replays.
 """
 
 import numpy as np
@@ -25,6 +26,7 @@ from kernels import linear as L
 pytestmark = pytest.mark.gpu
 
 V, K = 151936, 4096
+STREAM = _native.Config(_native.KIND_STREAM, 0, 0, 0, 0)  # the STREAM kind's default launch shape
 
 
 def _gathered(m, config=None, prologue=True):
@@ -54,8 +56,8 @@ def _check(ids, top, logits, m):
 
 def test_every_kind_in_one_sequence_shares_the_workspace(cuda, head):
     w, g = head
-    cases = [(1, None), (5, None), (2, None), (1, _native.Config(_native.KIND_GEMV, 2, 2, 8, 4)), (16, None),
-             (1, None), (8, _native.Config(_native.KIND_QUAD, 16, 0, 1, 8)), (5, None), (1, None)]
+    cases = [(1, STREAM), (5, None), (2, None), (1, _native.Config(_native.KIND_GEMV, 2, 2, 8, 4)), (16, None),
+             (1, None), (8, _native.Config(_native.KIND_QUAD, 16, 0, 1, 8)), (5, None), (1, STREAM), (1, None)]
     kinds = set()
     for i, (m, config) in enumerate(cases):
         x = seeded((m, K), seed=310 + i, device=cuda)
@@ -91,13 +93,17 @@ def test_graph_of_gathered_and_two_launch_calls_replays_to_the_eager_ids(cuda, h
     w, g = head
     xs = {m: seeded((m, K), seed=330 + m, device=cuda) for m in (1, 5)}
     tops = {m: torch.empty(m, dtype=torch.float32, device=cuda) for m in (1, 5)}
-    eager = {m: A.lm_head_argmax(xs[m], w, g, 1e-6, logits=False, top=tops[m])[0].clone() for m in (1, 5)}
+    cfgs = {1: STREAM, 5: None}
+    assert _gathered(1, STREAM)[0] and not _gathered(5)[0]
+    eager = {m: A.lm_head_argmax(xs[m], w, g, 1e-6, logits=False, top=tops[m], config=cfgs[m])[0].clone()
+             for m in (1, 5)}
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
-            out = {m: A.lm_head_argmax(xs[m], w, g, 1e-6, logits=False, top=tops[m])[0] for m in (1, 5)}
+            out = {m: A.lm_head_argmax(xs[m], w, g, 1e-6, logits=False, top=tops[m], config=cfgs[m])[0]
+                   for m in (1, 5)}
     torch.cuda.synchronize()
     other = seeded((2, K), seed=340, device=cuda)
     for r in range(4):

@@ -1,5 +1,5 @@
 """GPU tests of the RING kind's claimed tail: where a workgroup walks kRingTailMinTiles (16) or
-more tiles (lm_head + argmax at 5..16 rows), the last eighth of the tiles is claimed from a counter
+more tiles (lm_head + argmax with the norm prologue, at 1..16 rows), the last eighth of the tiles is claimed from a counter
 in the projection workspace, two tiles ahead of use, so that the workgroups that run ahead take
 more of them.
 
@@ -50,7 +50,7 @@ def head(cuda):
                                                                          device=cuda))
 
 
-@pytest.mark.parametrize("m", [5, 16])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 16])
 def test_claimed_tail_calls_in_a_row_match_the_oracle(cuda, head, m):
     w, g = head
     p = L.plan(m, w.shape[0], K, _native.EPI_ARGMAX, prologue=True)
@@ -73,9 +73,9 @@ def test_claimed_tail_calls_in_a_row_match_the_oracle(cuda, head, m):
         assert np.array_equal(top.cpu().numpy(), bf16.to_f32(got_logits)[np.arange(m), ids]), f"call {call}"
 
 
-def test_claimed_tail_graph_replays_equal_eager(cuda, head):
+@pytest.mark.parametrize("m", [1, 5])
+def test_claimed_tail_graph_replays_equal_eager(cuda, head, m):
     w, g = head
-    m = 5
     x = seeded((m, K), seed=9300, device=cuda)
     want_ids, want_logits = A.lm_head_argmax(x, w, g, EPS, logits=True, ids_dtype=torch.int32)
     want_ids, want_logits = want_ids.clone(), want_logits.clone()

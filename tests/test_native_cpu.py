@@ -258,7 +258,7 @@ RING_LONG = ((12, 8, 2), (12, 8, 3))
 
 
 def _ring_status(m, k, epilogue, kw, d, pro=False, rows=16):
-    if not 2 <= m <= 16 or k % (128 * kw):
+    if not 1 <= m <= 16 or k % (128 * kw):
         return _native.FTK_ERR_UNSUPPORTED
     c = k // (128 * kw)
     if rows == 24:  # 24-row tiles: STORE, up to 8 x rows, C = 4
@@ -289,7 +289,7 @@ def _configs(m):
                  for rs, _, kw in QUAD_SHAPES + QUAD_ONE for gpc in (1, 8)]
         gemv += [_native.Config(_native.KIND_STAGE, 16 * t, u, gpc, kw)
                  for t, _, kw, u in STAGE_EVEN + STAGE_ONE + STAGE_LONG for gpc in (1, 4)]
-    if 2 <= m <= 16:
+    if m <= 16:
         gemv += [_native.Config(_native.KIND_RING, rows, d, gpc, kw) for _, kw, d in RING_SHAPES + RING_LONG
                  for gpc in (1, 4) for rows in (12, 16, 24)]
     mfma = [_native.Config(_native.KIND_MFMA, rows, u, 0, w)
@@ -363,8 +363,7 @@ def test_plan_writes_every_output_once(m, n, k):
                 assert p.threads == 64 * p.waves and k % (128 * p.waves) == 0
             if p.kind == _native.KIND_RING:
                 # one workgroup per CU (groups_per_cu of them), 12, 16 or 24 weight rows per tile, any walk depth
-                default_gpc = 2 if epilogue == _native.EPI_ARGMAX else 1  # lm_head: two rounds
-                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else default_gpc
+                gpc = cfg.groups_per_cu if cfg is not None and cfg.groups_per_cu else 1
                 assert 1 <= p.grid <= min(p.tiles, 256 * gpc) and p.rows_per_wave in (12, 16, 24)
                 assert p.tiles == -(-(n // 2 if epilogue == _native.EPI_SWIGLU else n) //
                                     (8 if epilogue == _native.EPI_SWIGLU else p.rows_per_wave))
@@ -385,10 +384,22 @@ def test_plan_kinds():
     assert p.kind == _native.KIND_STREAM and p.threads == 256 and p.unroll * 512 * p.waves == 4096
     _native.call("ftk_plan_project", 1, 4096, 4104, 0, 256, None, p)  # K % 512 != 0: the LDS-staged GEMV
     assert p.kind == _native.KIND_GEMV and p.threads == 256
+    # lm_head + argmax without the norm prologue (no claimed-tail build): QUAD from 2 rows, STREAM at 1
     _native.call("ftk_plan_project", 4, 151936, 4096, _native.EPI_ARGMAX, 256, None, p)
     assert p.kind == _native.KIND_QUAD and -(-p.tiles // p.grid) <= 8
     _native.call("ftk_plan_project", 1, 151936, 4096, _native.EPI_ARGMAX, 256, None, p)
     assert p.kind == _native.KIND_STREAM and -(-p.tiles // p.grid) <= 8
+    # with the prologue: RING from one row, one round of workgroups whose walks end in claimed tiles
+    for m in (1, 2, 4):
+        _native.call("ftk_plan_project", m, 151936, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
+        assert p.kind == _native.KIND_RING and p.grid == 256 and p.tiles == 9496, m
+        assert p.workspace_bytes >= 256 + 256 * m * 8
+    # a vocabulary too short for 16 tiles per CU, or a K without a claimed-tail build: STREAM at one row
+    _native.call("ftk_plan_project", 1, 16 * 16 * 256 - 16, 4096, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256,
+                 None, p)
+    assert p.kind == _native.KIND_STREAM
+    _native.call("ftk_plan_project", 1, 151936, 2048, _native.EPI_ARGMAX | _native.PLAN_PROLOGUE, 256, None, p)
+    assert p.kind == _native.KIND_STREAM
     _native.call("ftk_plan_project", 1, 173, 259, 0, 256, None, p)
     assert p.kind == _native.KIND_GENERIC
     # rows of <= 3072 elements at one x row: one wave per row group (KW = 1), one tile per workgroup
@@ -449,9 +460,9 @@ def test_plan_kinds():
 
 def test_default_kind_for_8b_shapes():
     """The planner's choice at the Qwen3-8B shapes (from the MI355X sweeps): STREAM at M = 1 and,
-    to M = 4, except lm_head from 2 rows, gate/up from 3 and QKV at 4 (QUAD); RING for every
-    projection, SwiGLU and lm_head + argmax at 5..16 (the 8-row STREAM kernel where K = 12288 has
-    the prologue)."""
+    to M = 4, except gate/up from 3 and QKV at 4 (QUAD); RING for every projection and SwiGLU at
+    5..16 (the 8-row STREAM kernel where K = 12288 has the prologue) and for lm_head + argmax
+    (with the norm prologue) at every row count, its long walks ending in claimed tiles."""
     shapes = {"qkv": (6144, 4096, _native.EPI_STORE, True), "o": (4096, 4096, _native.EPI_STORE, False),
               "gate_up": (24576, 4096, _native.EPI_SWIGLU, True), "down": (4096, 12288, _native.EPI_STORE, False),
               "lm_head": (151936, 4096, _native.EPI_ARGMAX, True)}
@@ -460,8 +471,10 @@ def test_default_kind_for_8b_shapes():
             p = _native.Plan()
             flags = epi | (_native.PLAN_PROLOGUE if pro else 0)
             _native.call("ftk_plan_project", m, n, k, flags, 256, None, p)
-            quad_early = {"lm_head": 2, "gate_up": 3, "qkv": 4}.get(name, 5)
-            if m < quad_early:
+            quad_early = {"gate_up": 3, "qkv": 4}.get(name, 5)
+            if name == "lm_head":
+                want = _native.KIND_RING
+            elif m < quad_early:
                 want = _native.KIND_STREAM
             elif m <= 4:
                 want = _native.KIND_QUAD
