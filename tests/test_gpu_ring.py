@@ -1,4 +1,4 @@
-"""GPU parity of the RING kind (M = 2..16: weight and x segments loaded straight into a per-wave LDS
+"""GPU parity of the RING kind (M = 1..16: weight and x segments loaded straight into a per-wave LDS
 ring, 16x16x32 MFMAs).
 
 Against the CPU oracle: |y - ref| <= 2e-2 + 1e-2|ref| for every epilogue, with and without the
@@ -43,7 +43,7 @@ def _inputs(m, n, k, seed, device):
     return x, w, g
 
 
-@pytest.mark.parametrize("m", [2, 5, 8, 9, 16])
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 9, 16])
 def test_store_matches_oracle(cuda, m):
     n, k = 1000 + 5, 4096  # ragged last tile
     x, w, g = _inputs(m, n, k, seed=5000 + m, device=cuda)
@@ -134,7 +134,7 @@ def test_shapes_the_ring_does_not_take_are_refused(cuda):
     for m, k, depth, epilogue, pro in ((16, 12288, 3, _native.EPI_STORE, False),  # 16 x rows x 3 units: no LDS
                                        (5, 12288, 2, _native.EPI_STORE, True),    # no prologue at K = 12288
                                        (5, 4096, 3, _native.EPI_STORE, False),    # 3 does not divide C = 4
-                                       (1, 4096, 2, _native.EPI_STORE, False)):   # one row: the STREAM kinds
+                                       (17, 4096, 2, _native.EPI_STORE, False)):  # past 16 rows
         status = _native.lib().ftk_plan_project(m, 4096, k, epilogue | (_native.PLAN_PROLOGUE if pro else 0),
                                                 256, cfg(depth), _native.Plan())
         assert status != _native.FTK_OK, (m, k, depth, pro)
