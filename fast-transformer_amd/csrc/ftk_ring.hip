@@ -8,12 +8,13 @@
 // greedy argmax engine/kernels/argmax.py:19-48), FP32 accumulation, one rounding.
 //
 // Why: at 5..16 rows the kernels that hold x in registers spend as many L2
-// requests on x as on the weights. (Below 5 rows the planner takes this kind for
-// lm_head + argmax only, whose long walks end in the claimed tail.) An MFMA B operand needs x row l % 16 in lane
+// requests on x as on the weights. An MFMA B operand needs x row l % 16 in lane
 // l, so a register load of it touches 16 rows x 64 bytes per wave instruction.
 // Here x travels like the weights, 4 rows x 256 contiguous bytes per wave
 // instruction, straight into LDS, and is read back in MFMA layout. The weight
-// window lives in LDS too, so it costs no registers.
+// window lives in LDS too, so it costs no registers. (Below 5 rows the planner
+// takes this kind for lm_head + argmax only, whose long walks end in the
+// claimed tail.)
 //
 // Layout and schedule:
 //   * A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows)
