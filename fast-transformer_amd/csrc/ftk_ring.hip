@@ -150,6 +150,12 @@ __device__ __forceinline__ uint32_t lds_read_u32(const uint32_t* p) {
 }
 // An agent-scope atomic add returning the old value, as assembly: the compiler does
 // not count it, so it adds no wait of its own; the walk's exact waits return it.
+// Like every load written as assembly, the compiler takes its destination as
+// written at issue, so nothing may copy or reuse that register before the wait:
+// the claim's one value (claim_v) must stay in place across the walk's loop. The
+// claimed-tail builds' assembly holds it in one register throughout (checked when
+// this was written); a change that makes the compiler move it would read the claim
+// before it returns.
 __device__ __forceinline__ uint32_t claim_add(unsigned* p) {
   uint32_t old;
   asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(old) : "v"(p), "v"(1u) : "memory");
