@@ -1,7 +1,9 @@
 """The lm_head + argmax entry point that allocates nothing (ftk_lm_head_argmax_static_bf16),
 called through the C ABI and checked against the workspace entry point (ftk_lm_head_argmax_bf16):
-same ids, logits and top logits bit for bit, on two calls in a row (the second smaller), and
-a call beyond its static scratch rejected before any launch."""
+same ids, logits and top logits bit for bit, on calls in a row (each smaller than the one before;
+the first two on the RING kind, whose walks claim their last tiles from a counter in the static
+scratch that the previous call left at zero), and a call beyond its static scratch rejected
+before any launch."""
 
 import ctypes
 
@@ -42,8 +44,9 @@ def _run(name, x, w, gamma, logits, ids, top, workspace=None):
 
 
 def test_static_scratch_matches_the_workspace_entry_point(cuda):
-    # two calls in a row, the second with fewer rows, a smaller vocabulary and no prologue gain
-    cases = ((4, 151936, 4096, torch.int32, True), (1, 50000, 2048, torch.int64, False))
+    # calls in a row, each smaller: fewer rows, then a smaller vocabulary and no prologue gain
+    cases = ((4, 151936, 4096, torch.int32, True), (1, 151936, 4096, torch.int64, True),
+             (1, 50000, 2048, torch.int64, False))
     for m, v, k, ids_dtype, with_gamma in cases:
         print(f"static scratch lm_head case M={m} V={v} K={k} ids={ids_dtype}", flush=True)
         x, w, gamma = _inputs(m, v, k, 7000 + m, cuda)
