@@ -508,3 +508,25 @@ def test_residual_calls_size_the_workspace_of_their_own_plan(m):
     assert with_residual == p.workspace_bytes >= 256 + 8 * m * p.grid
     _native.call("ftk_plan_project", m, 151936, 4096, flags, 256, None, p)
     assert p.kind == _native.KIND_RING and plain == p.workspace_bytes
+
+
+@pytest.mark.parametrize("cus", [64, 80, 100, 104, 228, 256, 304])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 16])
+def test_lm_head_plans_on_other_cu_counts(cus, m):
+    """lm_head + argmax with the norm on devices of other CU counts (partitions, other parts): the
+    plan writes every logit once, its argmax keys fit the workspace, and a RING plan whose walks are
+    long enough for the claimed tail (at least 16 tiles per workgroup, as the kernel decides) has
+    room for the claim counter; below 5 rows RING is chosen only where those walks are that long."""
+    v, k = 151936, 4096
+    flags = _native.EPI_ARGMAX | _native.PLAN_PROLOGUE
+    p = _native.Plan()
+    assert _native.lib().ftk_plan_project(m, v, k, flags, cus, None, p) == _native.FTK_OK
+    counts, max_row = _coverage(p, v, _native.EPI_ARGMAX)
+    assert np.all(counts == 1) and max_row == v - 1
+    assert p.workspace_bytes >= 256 + 8 * m * p.grid
+    if p.kind == _native.KIND_RING:
+        assert 1 <= p.grid <= p.tiles
+        if p.tiles >= 16 * p.grid:
+            assert p.workspace_bytes >= 128 + 4
+        if m < 5:
+            assert p.tiles >= 16 * cus
